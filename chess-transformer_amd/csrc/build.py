@@ -1,0 +1,52 @@
+"""Builds libchess_hip.so, the gfx950 kernels and their C ABI (include/chess_hip.h), with hipcc.
+
+python chess-transformer_amd/csrc/build.py  -- or __graft_entry__.build().
+The library is written next to the package (chess-transformer_amd/libchess_hip.so), where the
+loader (model/hip_kernels.py) looks for it; objects go to csrc/_build/.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+CSRC = Path(__file__).resolve().parent
+PACKAGE = CSRC.parent
+LIBRARY = PACKAGE / "libchess_hip.so"
+OBJECTS = CSRC / "_build"
+SOURCES = ["runtime.hip", "norm_quant.hip", "rotate_quant.hip", "int8_gemm.hip", "attention.hip", "linear_f16.hip"]
+ARCH = "gfx950"
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+# -ffp-contract=off and IEEE divide/sqrt: the f32 op order the kernels declare is what runs.
+# -packed-fp32-ops off: hipcc would otherwise pair f32 ops into v_pk_* instructions by itself.
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
+
+
+def compile_one(source: str) -> Path:
+    target = OBJECTS / (Path(source).stem + ".o")
+    command = [HIPCC, *FLAGS, "-c", str(CSRC / source), "-o", str(target)]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {source}:\n{result.stdout}{result.stderr}")
+    return target
+
+
+def build(output: Path = LIBRARY, jobs: int | None = None) -> Path:
+    OBJECTS.mkdir(exist_ok=True)
+    with ThreadPoolExecutor(jobs or min(8, os.cpu_count() or 1)) as pool:
+        objects = list(pool.map(compile_one, SOURCES))
+    partial = output.with_name(output.name + f".{os.getpid()}.partial")
+    command = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(partial), *map(str, objects)]
+    result = subprocess.run(command, capture_output=True, text=True)
+    if result.returncode != 0:
+        raise RuntimeError(f"hipcc failed to link {output.name}:\n{result.stdout}{result.stderr}")
+    os.replace(partial, output)
+    return output
+
+
+if __name__ == "__main__":
+    print(build())
+    sys.exit(0)

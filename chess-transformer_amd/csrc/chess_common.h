@@ -1,0 +1,91 @@
+// Shared device helpers for the gfx950 kernels of the int8 network evaluation.
+//
+// Arithmetic contract: the library is built with -ffp-contract=off and IEEE
+// (correctly rounded) f32 divide and sqrt, so every f32 expression below is the
+// sequence of single IEEE operations it spells -- the CPU restatement under
+// oracle/ computes the same sequence with numpy and gets the same bits.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef _Float16 v8h __attribute__((ext_vector_type(8)));
+typedef _Float16 v4h __attribute__((ext_vector_type(4)));
+
+#define DEVICE __device__ __forceinline__
+
+// Error codes beyond HIP's own (hipError_t values stay below 1000).
+enum {
+    CHESS_OK = 0,
+    CHESS_INVALID_SHAPE = 1001,
+    CHESS_MISALIGNED = 1002,
+    CHESS_UNSUPPORTED = 1003,
+};
+
+// Output element types of the GEMM epilogues.
+enum { OUT_F16 = 0, OUT_BF16 = 1, OUT_F32 = 2 };
+
+struct bf16_t { uint16_t bits; };
+
+DEVICE float to_float(half_t v) { return (float)v; }
+DEVICE float to_float(bf16_t v) { return __uint_as_float(((uint32_t)v.bits) << 16); }
+DEVICE float to_float(float v) { return v; }
+
+// f32 -> bf16, round to nearest even; a NaN stays a quiet NaN.
+DEVICE bf16_t bf16_from_float(float f) {
+    uint32_t bits = __float_as_uint(f);
+    bf16_t out;
+    if ((bits & 0x7fffffffu) > 0x7f800000u) {
+        out.bits = (uint16_t)((bits >> 16) | 0x40u);
+    } else {
+        out.bits = (uint16_t)((bits + 0x7fffu + ((bits >> 16) & 1u)) >> 16);
+    }
+    return out;
+}
+
+template <typename T> DEVICE T from_float(float f);
+template <> DEVICE half_t from_float<half_t>(float f) { return (half_t)f; }
+template <> DEVICE bf16_t from_float<bf16_t>(float f) { return bf16_from_float(f); }
+template <> DEVICE float from_float<float>(float f) { return f; }
+
+// silu(g) = g / (1 + 2^(-g log2 e)) from the hardware's exp2 (v_exp_f32) and reciprocal (v_rcp_f32):
+// a few VALU ops, so the gated epilogue stays hidden under the MFMA work of a K=512 GEMM.
+DEVICE float silu_fast(float g) {
+    return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f));
+}
+
+// xor butterflies over the 64 lanes of a wavefront: every lane ends with the same bits,
+// the balanced tree of adjacent lane pairs (a + b == b + a bitwise).
+DEVICE float wave_sum(float v) {
+#pragma unroll
+    for (int offset = 1; offset < 64; offset <<= 1) v = v + __shfl_xor(v, offset, 64);
+    return v;
+}
+
+DEVICE float wave_max(float v) {
+#pragma unroll
+    for (int offset = 1; offset < 64; offset <<= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+    return v;
+}
+
+// Maps a workgroup id so that consecutive tiles land on one XCD: the hardware deals
+// workgroups to the 8 XCDs round-robin, and each XCD has its own L2.
+DEVICE int xcd_local_tile(int wg, int tiles) {
+    constexpr int XCDS = 8;
+    if (tiles % XCDS != 0) return wg;
+    return (wg % XCDS) * (tiles / XCDS) + wg / XCDS;
+}
+
+// Host-side launch-result check shared by the entry points.
+static inline int launch_status() {
+    hipError_t error = hipGetLastError();
+    return error == hipSuccess ? CHESS_OK : (int)error;
+}
+
+// Records a message for chess_last_error() and returns code.
+int chess_fail(int code, const char* format, ...);
+
+static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

@@ -1,0 +1,109 @@
+// Block-Hadamard rotation + per-row int8 quantisation of the mlp's hidden rows.
+// Computes what model/int8_blocks.py:216-246 (rotate_quant_kernel) does, in a declared op order:
+// h[M, N] (fp16) is zero-padded to WIDTH columns; each 32-column block is multiplied by Sylvester's
+// H32 as five f32 butterfly stages of spans 1, 2, 4, 8, 16, (a, b) -> (a + b, a - b); then
+// absmax = max(max |r|, 1e-20), q = rint(r * (127 / absmax)), scale = absmax / 127.
+// One wavefront per row. A lane holds 8 consecutive columns (16 bytes) per pass of 512 columns, so
+// four lanes hold a 32-block: spans 1-4 run in the lane, spans 8 and 16 with lanes ^1 and ^2.
+// Bandwidth-bound: 2N bytes in, WIDTH + 4 out per row.
+#include "chess_common.h"
+
+namespace {
+
+constexpr int ROWS_PER_BLOCK = 4;
+constexpr int LANE_COLUMNS = 8;
+constexpr int PASS_COLUMNS = 64 * LANE_COLUMNS;
+
+// a pass's 8 columns: the first three butterfly stages in the lane, the last two across lanes
+DEVICE void butterflies(float (&v)[LANE_COLUMNS], int lane) {
+#pragma unroll
+    for (int span = 1; span < LANE_COLUMNS; span <<= 1)
+#pragma unroll
+        for (int i = 0; i < LANE_COLUMNS; i++)
+            if ((i & span) == 0) {
+                const float a = v[i], b = v[i + span];
+                v[i] = a + b;
+                v[i + span] = a - b;
+            }
+#pragma unroll
+    for (int bit = 0; bit < 2; bit++) {
+        const bool upper = (lane >> bit) & 1;
+#pragma unroll
+        for (int i = 0; i < LANE_COLUMNS; i++) {
+            const float other = __shfl_xor(v[i], 1 << bit, 64);
+            v[i] = upper ? other - v[i] : v[i] + other;
+        }
+    }
+}
+
+template <int PASSES>
+__global__ __launch_bounds__(64 * ROWS_PER_BLOCK) void rotate_quant_kernel(
+    const half_t* __restrict__ h, int8_t* __restrict__ q, float* __restrict__ scale, int M, int N, int width)
+{
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
+    if (row >= M) return;
+    const half_t* from = h + (size_t)row * N;
+    const bool vector = N % LANE_COLUMNS == 0;
+
+    float v[PASSES][LANE_COLUMNS];
+    float largest = 0.0f;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; pass++) {
+        const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
+        half_t raw[LANE_COLUMNS];
+        if (vector && col < N) {
+            *reinterpret_cast<uint4*>(raw) = *reinterpret_cast<const uint4*>(from + col);
+        } else {
+#pragma unroll
+            for (int i = 0; i < LANE_COLUMNS; i++) raw[i] = col + i < N ? from[col + i] : (half_t)0.0f;
+        }
+#pragma unroll
+        for (int i = 0; i < LANE_COLUMNS; i++) v[pass][i] = (float)raw[i];
+        butterflies(v[pass], lane);
+#pragma unroll
+        for (int i = 0; i < LANE_COLUMNS; i++) largest = fmaxf(largest, fabsf(v[pass][i]));
+    }
+    const float absmax = fmaxf(wave_max(largest), 1e-20f);
+    const float inverse_step = 127.0f / absmax;
+    int8_t* to = q + (size_t)row * width;
+#pragma unroll
+    for (int pass = 0; pass < PASSES; pass++) {
+        const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
+        if (col >= width) continue;
+        int8_t out[LANE_COLUMNS];
+#pragma unroll
+        for (int i = 0; i < LANE_COLUMNS; i++) out[i] = (int8_t)(int)__builtin_rintf(v[pass][i] * inverse_step);
+        *reinterpret_cast<uint2*>(to + col) = *reinterpret_cast<const uint2*>(out);
+    }
+    if (lane == 0) scale[row] = absmax / 127.0f;
+}
+
+template <int PASSES> int launch(const void* h, void* q, void* scale, int M, int N, int width, hipStream_t stream) {
+    const dim3 grid((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK), block(64 * ROWS_PER_BLOCK);
+    hipLaunchKernelGGL(rotate_quant_kernel<PASSES>, grid, block, 0, stream, (const half_t*)h, (int8_t*)q, (float*)scale, M, N, width);
+    return launch_status();
+}
+
+}  // namespace
+
+extern "C" int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int width, void* stream)
+{
+    if (M < 0 || N <= 0 || width < N || width % 32 != 0)
+        return chess_fail(CHESS_INVALID_SHAPE, "rotate_quant pads %d columns to a width divisible by 32, not %d", N, width);
+    if (width > 8 * PASS_COLUMNS) return chess_fail(CHESS_UNSUPPORTED, "rotate_quant takes widths up to %d, not %d", 8 * PASS_COLUMNS, width);
+    if (!h || !q || !scale) return chess_fail(CHESS_INVALID_SHAPE, "rotate_quant: a required pointer is null");
+    if (!aligned16(h) || !aligned16(q)) return chess_fail(CHESS_MISALIGNED, "rotate_quant's vector loads need 16-byte aligned rows");
+    if (M == 0) return CHESS_OK;
+    hipStream_t s = (hipStream_t)stream;
+    switch ((width + PASS_COLUMNS - 1) / PASS_COLUMNS) {
+        case 1: return launch<1>(h, q, scale, M, N, width, s);
+        case 2: return launch<2>(h, q, scale, M, N, width, s);
+        case 3: return launch<3>(h, q, scale, M, N, width, s);
+        case 4: return launch<4>(h, q, scale, M, N, width, s);
+        case 5: return launch<5>(h, q, scale, M, N, width, s);
+        case 6: return launch<6>(h, q, scale, M, N, width, s);
+        case 7: return launch<7>(h, q, scale, M, N, width, s);
+        default: return launch<8>(h, q, scale, M, N, width, s);
+    }
+}

@@ -1,0 +1,242 @@
+"""fp16 blocks and the template attention on gfx950: the module API of the reference's model/fused_blocks.py
+that the int8 path uses -- the operators chess::template_attention and chess::linear, FusedBlock,
+link_input_mixes, tile_for -- and FusedTransformer, the network the engine calls.
+
+The operators launch the HIP kernels of libchess_hip.so. The heads and the input embedding run as
+torch operations on the GPU, which is the reference's own path on GPUs without its fused ends
+(reference fused_blocks.py:515-529, 863-874; on ROCm fused_ends is never true).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from model import hip_kernels
+from model.encoding import NUM_SQUARES, TOKENS_PER_BOARD
+from model.hip_kernels import aligned, check, library_for, pointer, stream_of
+from model.model import ChessTransformer, TransformerBlock
+
+LINEAR_DEPTH, GROUP_M = 32, 8
+# linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185): 1 has 64-row tiles, 2 128-row
+LINEAR_TILES = {"gfx950": [(64, 1), (math.inf, 2)]}
+# positions a launch should reach before a workgroup takes several key/value groups
+ATTENTION_WORKGROUPS = 1024
+
+
+#the first of [(the most rows a multiprocessor's share may be, tile), ...] that the share fits, the last taking any
+def tile_for(tiles: list[tuple[float, object]], M: int, multiprocessors: int):
+    share = M / multiprocessors
+    return next(tile for most, tile in tiles if share <= most)
+
+
+def linear_tile(device: torch.device, M: int) -> int:
+    arch = torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
+    return tile_for(LINEAR_TILES.get(arch, LINEAR_TILES["gfx950"]), M, torch.cuda.get_device_properties(device).multi_processor_count)
+
+
+def groups_per_workgroup(positions: int, kv_heads: int) -> int:
+    """The most key/value groups a workgroup takes while the launch keeps ATTENTION_WORKGROUPS workgroups; any choice gives the same bits."""
+    best = 1
+    for groups in range(1, kv_heads + 1):
+        if kv_heads % groups == 0 and positions * (kv_heads // groups) >= ATTENTION_WORKGROUPS:
+            best = groups
+    return best
+
+
+def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, heads: int, kv_heads: int,
+                              dq: int, dv: int, templates_count: int, eps: float, groups_per_block: int | None = None) -> torch.Tensor:
+    for tensor, name in ((projected, "projected"), (templates, "templates"), (q_gain, "q_gain"), (k_gain, "k_gain")):
+        if tensor.dtype != torch.float16:
+            raise ValueError(f"template_attention's {name} is {tensor.dtype}, the kernel takes fp16")
+    B, T, width = projected.shape
+    if width != heads * dq + kv_heads * dq + kv_heads * dv + heads * templates_count:
+        raise ValueError(f"template_attention: rows of {width} are not q | k | v | template mix for {heads} heads, {kv_heads} key/value heads, "
+                         f"widths {dq} and {dv}, {templates_count} templates")
+    if templates.shape[0] < templates_count or tuple(templates.shape[1:]) != (NUM_SQUARES, NUM_SQUARES):
+        raise ValueError(f"template_attention takes {templates_count} templates of 64 x 64, not {tuple(templates.shape)}")
+    library = library_for(projected.device)
+    projected = aligned(projected)
+    templates = aligned(templates)
+    out = torch.empty(B, T, heads * dv, device=projected.device, dtype=torch.float16)
+    groups = groups_per_block or groups_per_workgroup(B, kv_heads)
+    code = library.chess_template_attention(pointer(projected), pointer(templates), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()),
+                                            pointer(out), B, T, heads, kv_heads, dq, dv, templates_count, groups, float(eps), 1 / math.sqrt(dq),
+                                            stream_of(projected.device))
+    check(code, "template_attention")
+    return out
+
+
+#an opaque op, so that torch.compile does not compile through the kernel calls
+@torch.library.custom_op("chess::template_attention", mutates_args=())
+def template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, heads: int, kv_heads: int,
+                       dq: int, dv: int, templates_count: int, eps: float) -> torch.Tensor:
+    return launch_template_attention(projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_count, eps)
+
+
+@template_attention.register_fake
+def _(projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_count, eps):
+    B, T, _ = projected.shape
+    return projected.new_empty(B, T, heads * dv)
+
+
+def launch_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, residual: torch.Tensor | None, gated: bool,
+                  accumulate_fp32: bool, original: torch.Tensor | None, residual_scale: torch.Tensor | None, input_scale: torch.Tensor | None,
+                  tile: int = 0) -> torch.Tensor:
+    K, width = weight.shape
+    N = width // 2 if gated else width
+    if K % LINEAR_DEPTH != 0:
+        raise ValueError(f"linear reads the {K} inputs {LINEAR_DEPTH} at a time")
+    if x.shape[-1] != K:
+        raise ValueError(f"linear: x has {x.shape[-1]} inputs and the weight {K}")
+    for tensor, name in ((x, "x"), (weight, "weight"), (bias, "bias"), (residual, "residual"), (original, "original"),
+                         (residual_scale, "residual_scale"), (input_scale, "input_scale")):
+        if tensor is not None and tensor.dtype != torch.float16:
+            raise ValueError(f"linear's {name} is {tensor.dtype}, the kernel takes fp16")
+    library = library_for(x.device)
+    x, weight, residual, original = aligned(x), aligned(weight), aligned(residual), aligned(original)
+    M = x.numel() // K
+    out = x.new_empty(*x.shape[:-1], N, dtype=torch.float32 if accumulate_fp32 else torch.float16)
+    code = library.chess_linear(pointer(x), pointer(weight), pointer(bias.contiguous() if bias is not None else None), pointer(residual),
+                                pointer(original), pointer(residual_scale), pointer(input_scale), pointer(out), M, N, K, int(gated),
+                                hip_kernels.OUT_F32 if accumulate_fp32 else hip_kernels.OUT_F16, tile, stream_of(x.device))
+    check(code, "linear")
+    return out
+
+
+#fp16 inputs, f32 sums; fp16 out, or f32 with accumulate_fp32 (reference fused_blocks.py:307-313)
+@torch.library.custom_op("chess::linear", mutates_args=())
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+           gated: bool = False, accumulate_fp32: bool = False, original: torch.Tensor | None = None, residual_scale: torch.Tensor | None = None,
+           input_scale: torch.Tensor | None = None) -> torch.Tensor:
+    tile = linear_tile(x.device, x.numel() // weight.shape[0])
+    return launch_linear(x, weight, bias, residual, gated, accumulate_fp32, original, residual_scale, input_scale, tile)
+
+
+@linear.register_fake
+def _(x, weight, bias=None, residual=None, gated=False, accumulate_fp32=False, original=None, residual_scale=None, input_scale=None):
+    return x.new_empty(*x.shape[:-1], weight.shape[1] // 2 if gated else weight.shape[1], dtype=torch.float32 if accumulate_fp32 else x.dtype)
+
+
+def transposed(weight: torch.Tensor) -> nn.Parameter:
+    return nn.Parameter(weight.detach().t().contiguous())
+
+
+class FusedBlock(nn.Module):
+    """A TransformerBlock's weights as the fused kernels read them (reference fused_blocks.py:325-354):
+    projection = [Q | K | V | template_mix] transposed, gate_up = [gate | up] transposed."""
+
+    def __init__(self, block: TransformerBlock):
+        super().__init__()
+        self.heads, self.kv_heads = block.n_heads, block.kv_heads
+        self.dq, self.dv, self.templates_count = block.d_qk_head, block.d_head, block.position_templates
+        self.ln1, self.ln2 = block.ln1, block.ln2
+        self.residual_scale, self.input_scale = block.residual_scale, block.input_scale
+        self.q_gain, self.k_gain = block.q_norm.weight, block.k_norm.weight
+        self.eps = block.q_norm.eps
+        projections = (block.Q, block.K, block.V, block.template_mix)
+        mlp = block.mlp
+        self.projection = transposed(torch.cat([projection.weight for projection in projections]))
+        self.projection_bias = nn.Parameter(torch.cat([projection.bias for projection in projections]).detach())
+        self.combine_heads = transposed(block.combine_heads.weight)
+        self.combine_heads_bias = block.combine_heads.bias
+        self.gate_up = transposed(torch.cat([mlp.gate_projection.weight, mlp.up_projection.weight]))
+        self.down = transposed(mlp.down_projection.weight)
+        self.next_scales: tuple[nn.Parameter, nn.Parameter] | None = None
+        self.input_mixed = False
+
+    def forward(self, x: torch.Tensor, templates: torch.Tensor, original_board_embed: torch.Tensor) -> torch.Tensor:
+        if not self.input_mixed:
+            x = self.residual_scale * x + self.input_scale * original_board_embed
+        attended = template_attention(linear(self.ln1(x), self.projection, self.projection_bias), templates, self.q_gain, self.k_gain, self.heads,
+                                      self.kv_heads, self.dq, self.dv, self.templates_count, self.eps)
+        x = linear(attended, self.combine_heads, self.combine_heads_bias, residual=x)
+        hidden = linear(self.ln2(x), self.gate_up, gated=True)
+        if self.next_scales is None:
+            return linear(hidden, self.down, residual=x)
+        return linear(hidden, self.down, residual=x, original=original_board_embed, residual_scale=self.next_scales[0], input_scale=self.next_scales[1])
+
+
+#a down mixes the next block's input when both blocks are of one type; after a block of the other type, a block mixes its own input
+def link_input_mixes(blocks: list[nn.Module]) -> None:
+    for block in blocks:
+        block.next_scales, block.input_mixed = None, False
+    for block, following in zip(blocks, blocks[1:]):
+        if type(block) is type(following):
+            block.next_scales, following.input_mixed = (following.residual_scale, following.input_scale), True
+
+
+def prepare(templates: torch.Tensor) -> None:
+    """Nothing to prepare: the kernels read the templates as the model holds them (the reference paired them, attention_cuda.py:410-440)."""
+
+
+class InputEmbedding(nn.Module):
+    """Token + position embedding plus the square features, summed as the reference's input_embedding kernel sums them
+    (fused_blocks.py:370-393): the features' sum rounded to the table's precision first, then all three in f32."""
+
+    def __init__(self, model: ChessTransformer):
+        super().__init__()
+        self.embed, self.position_embed, self.features = model.embed, model.position_embed, model.square_features
+
+    def forward(self, board_state: torch.Tensor) -> torch.Tensor:
+        B = board_state.shape[0]
+        table = self.features.table
+        rows = self.features.indices(board_state) + self.features.row_offsets
+        features = F.embedding_bag(rows.reshape(B * NUM_SQUARES, -1), table.float(), mode="sum").to(table.dtype).reshape(B, NUM_SQUARES, -1)
+        total = self.embed.weight[board_state].float() + self.position_embed.float()
+        total[:, :NUM_SQUARES] += features.float()
+        return total.to(self.embed.weight.dtype)
+
+
+#logits[i, j] = (W_f x_i + b_f) . (W_t x_j + b_t) / sqrt(d) = a_i . x_j + s_i: from and to as one d x d matmul (a)
+def head_weights(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    with torch.no_grad():
+        from_weight, from_bias = model.from_projection.weight.double(), model.from_projection.bias.double()
+        to_weight, to_bias = model.to_projection.weight.double(), model.to_projection.bias.double()
+        promotion, down = model.promotion_projection, model.board_down_project[0]
+        scale = 1 / math.sqrt(model.d_model)
+        narrow_weight = torch.cat([(to_bias @ from_weight)[None] * scale, promotion.weight.double(), down.weight.double()])
+        narrow_bias = torch.cat([(from_bias @ to_bias)[None] * scale, promotion.bias.double(), down.bias.double()])
+        return ((from_weight.T @ to_weight * scale).half(), (to_weight.T @ from_bias * scale).float(), narrow_weight.float(), narrow_bias.float())
+
+
+class FusedTransformer(nn.Module):
+    """ChessTransformer.forward with FusedBlocks, for inference (reference fused_blocks.py:829-874, its path without fused ends):
+    returns the move logits and the value logits."""
+
+    def __init__(self, model: ChessTransformer):
+        super().__init__()
+        self.d_model = model.d_model
+        self.input_embedding = InputEmbedding(model)
+        self.templates, self.ln = model.templates, model.ln
+        self.encoder = nn.ModuleList(FusedBlock(block) for block in model.encoder)
+        link_input_mixes(list(self.encoder))
+        prepare(model.templates)
+        self.fused_heads = False
+        self.board_down_activation, self.eval_head = model.board_down_project[1], model.eval_head
+        for name in ("from_squares", "to_squares", "promotion_move_ids", "promotion_to_squares", "promotion_pieces"):
+            self.register_buffer(name, getattr(model, name))
+        self.a_weight, self.a_bias, self.narrow_weight, self.narrow_bias = (nn.Parameter(tensor, requires_grad=False) for tensor in head_weights(model))
+        promotions = model.promotion_projection.out_features
+        self.promotion_columns, self.down_columns = slice(1, 1 + promotions), slice(1 + promotions, None)
+
+    def forward(self, board_state: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        embed_state = self.input_embedding(board_state)
+        original_board_embed = embed_state
+        for block in self.encoder:
+            embed_state = block(embed_state, self.templates, original_board_embed)
+        model_output = self.ln(embed_state)
+
+        with torch.autocast(device_type=board_state.device.type, enabled=False):
+            #the f32 bias after the kernel, which takes fp16 biases
+            a = linear(model_output.half(), self.a_weight, accumulate_fp32=True) + self.a_bias
+            model_output = model_output.float()
+            narrow = F.linear(model_output, self.narrow_weight, self.narrow_bias)  #B T: s, the promotion logits, board_down_project's
+            squares = narrow[:, :NUM_SQUARES]
+            logits = a[:, :NUM_SQUARES] @ model_output[:, :NUM_SQUARES].transpose(1, 2).contiguous() + squares[..., :1]
+            combined_logits = logits[:, self.from_squares, self.to_squares]
+            combined_logits[:, self.promotion_move_ids] += squares[..., self.promotion_columns][:, self.promotion_to_squares, self.promotion_pieces]
+            compressed_board = self.board_down_activation(narrow[..., self.down_columns]).reshape(board_state.shape[0], -1)
+            return combined_logits, self.eval_head(compressed_board)

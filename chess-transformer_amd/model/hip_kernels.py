@@ -1,0 +1,97 @@
+"""The loader of libchess_hip.so, the gfx950 kernels behind the chess:: operators.
+
+Takes the place of the reference's two NVRTC/driver loaders (model/int8_cuda.py:213-344 and
+model/attention_cuda.py:346-407): there is nothing to compile at start-up and no cache of
+compiled code. The library is loaded once per process, after torch, so that it binds to the HIP
+runtime torch already loaded and its kernels run on torch's streams. There is no fallback: a
+missing library or a GPU that is not gfx950 raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIBRARY_PATH = Path(__file__).resolve().parent.parent / "libchess_hip.so"
+TARGET = "gfx950"
+
+INVALID_SHAPE, MISALIGNED, UNSUPPORTED = 1001, 1002, 1003
+OUT_F16, OUT_BF16, OUT_F32 = 0, 1, 2
+
+_pointer, _int, _float = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+SIGNATURES = {
+    "chess_norm_quant": [_pointer] * 8 + [_int, _int, _float, _pointer],
+    "chess_rotate_quant": [_pointer] * 3 + [_int] * 3 + [_pointer],
+    "chess_int8_linear": [_pointer] * 10 + [_int] * 6 + [_pointer],
+    "chess_int8_matmul_i32": [_pointer] * 3 + [_int] * 4 + [_pointer],
+    "chess_template_attention": [_pointer] * 5 + [_int] * 8 + [_float, _float, _pointer],
+    "chess_linear": [_pointer] * 8 + [_int] * 6 + [_pointer],
+    "chess_runtime_addresses": [ctypes.POINTER(ctypes.c_void_p), _int],
+    "chess_error_string": [_int],
+    "chess_last_error": [],
+    "chess_target": [],
+}
+STRINGS = ("chess_error_string", "chess_last_error", "chess_target")
+
+_lock = threading.Lock()
+_library: ctypes.CDLL | None = None
+_checked_devices: set[int] = set()
+
+
+def load_library(path: Path = LIBRARY_PATH) -> ctypes.CDLL:
+    """The library with its argument types; no GPU is touched (the CPU tests load it too)."""
+    global _library
+    with _lock:
+        if _library is None:
+            if not path.exists():
+                raise RuntimeError(f"{path} is not built: run `python chess-transformer_amd/csrc/build.py` (or __graft_entry__.build())")
+            # PyDLL: a launch only queues work, so it keeps the GIL and skips releasing it (as the reference's
+            # quick runtime calls do, engine/cuda_runtime.py:16, 33)
+            library = ctypes.PyDLL(str(path))
+            for name, arguments in SIGNATURES.items():
+                function = getattr(library, name)
+                function.argtypes = arguments
+                function.restype = ctypes.c_char_p if name in STRINGS else ctypes.c_int
+            _library = library
+        return _library
+
+
+def library_for(device: torch.device) -> ctypes.CDLL:
+    """The library, once the device is checked to be the GPU it was built for."""
+    library = load_library()
+    if device.type != "cuda":
+        raise ValueError(f"the chess:: operators run on the GPU, not on {device}")
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    if index not in _checked_devices:
+        arch = torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
+        if arch != TARGET:
+            raise RuntimeError(f"libchess_hip.so is built for {TARGET}, and device {index} is {arch}")
+        _checked_devices.add(index)
+    return library
+
+
+def check(code: int, what: str) -> None:
+    if code == 0:
+        return
+    library = load_library()
+    if code in (INVALID_SHAPE, MISALIGNED, UNSUPPORTED):
+        raise ValueError(f"{what}: {library.chess_last_error().decode()}")
+    raise RuntimeError(f"{what}: HIP error {code}, {library.chess_error_string(code).decode()}")
+
+
+def pointer(tensor: torch.Tensor | None) -> int | None:
+    return None if tensor is None else tensor.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def aligned(tensor: torch.Tensor | None) -> torch.Tensor | None:
+    """Contiguous and 16-byte aligned (the kernels' vector loads): a copy only when a view starts mid-row."""
+    if tensor is None:
+        return None
+    tensor = tensor.contiguous()
+    return tensor if tensor.data_ptr() % 16 == 0 else tensor.clone()

@@ -1,0 +1,271 @@
+"""Int8 transformer blocks on gfx950: the module API of the reference's model/int8_blocks.py.
+
+Same names, signatures, operator schemas (chess::int8_linear, chess::norm_quant,
+chess::mix_norm_quant, chess::rotate_quant) and Int8Block / quantize_blocks behaviour, so that
+engine/inference.py (int8_model, reference :267-272) and the MCTS that calls it run unchanged.
+Underneath, every operator is one launch of a hand-written HIP kernel from libchess_hip.so
+(csrc/): no Triton, no NVRTC, no fallback. A shape the kernels do not take raises ValueError
+where the reference fell back to another kernel (reference int8_cuda.py:369-381).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+from torch import nn
+
+from model import hip_kernels
+from model.fused_blocks import FusedBlock, linear, link_input_mixes, template_attention, tile_for
+from model.hip_kernels import aligned, check, library_for, pointer, stream_of
+
+# model/int8_blocks.py:14-17 of the reference: the mlp's hidden is rotated in blocks of 32 (H H^T = 32 I) and
+# zero-padded to a multiple of 128 for down
+HADAMARD_BLOCK = 32
+DOWN_INPUT_MULTIPLE = 128
+INT8_DEPTH = 64
+# The GEMM's tiles by the rows a compute unit's share is (the reference's table format, int8_blocks.py:19-31):
+# tile 1 has 64-row tiles, 2 has 128-row tiles. Every tile gives the same bits.
+SMALL_TILE, LARGE_TILE = 1, 2
+INT8_TILES = {"gfx950": {"projection": [(64, SMALL_TILE), (math.inf, LARGE_TILE)],
+                         "gate_up": [(64, SMALL_TILE), (math.inf, LARGE_TILE)],
+                         "down": [(128, SMALL_TILE), (math.inf, LARGE_TILE)]}}
+# rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit
+NORM_ROWS = 4
+ROTATE_ROWS = 4
+
+
+def gpu_arch(device: torch.device) -> str:
+    return torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
+
+
+def int8_tile(device: torch.device, matmul: str, M: int) -> int:
+    """The tile of int8_linear for M rows of matmul (reference int8_blocks.py:39-42, keyed by gfx target, not capability)."""
+    tiles = INT8_TILES.get(gpu_arch(device), INT8_TILES["gfx950"])[matmul]
+    return tile_for(tiles, M, torch.cuda.get_device_properties(device).multi_processor_count)
+
+
+def rotate_rows(device: torch.device, M: int) -> int:
+    return ROTATE_ROWS
+
+
+def hadamard(size: int) -> torch.Tensor:
+    """Sylvester's Hadamard matrix of +-1, size a power of two: symmetric, its square is size times the identity."""
+    if size <= 0 or size & (size - 1):
+        raise ValueError(f"a Sylvester Hadamard matrix has a power-of-two size, not {size}")
+    index = torch.arange(size)
+    ones = torch.bitwise_and(index[:, None], index[None, :])
+    parity = torch.zeros_like(ones)
+    while bool(ones.any()):
+        parity ^= ones & 1
+        ones = ones >> 1
+    return 1.0 - 2.0 * parity.float()
+
+
+def down_inputs(hidden: int) -> int:
+    return -(-hidden // DOWN_INPUT_MULTIPLE) * DOWN_INPUT_MULTIPLE
+
+
+def _require(tensor: torch.Tensor | None, dtype: torch.dtype, name: str) -> None:
+    if tensor is not None and tensor.dtype != dtype:
+        raise ValueError(f"{name} is {tensor.dtype}, the kernel takes {dtype}")
+
+
+def launch_int8_linear(x: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                       residual: torch.Tensor | None, gated: bool, original: torch.Tensor | None, residual_scale: torch.Tensor | None,
+                       input_scale: torch.Tensor | None, tile: int = 0, out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """out = epilogue(x @ weight^T) (x M x K, weight N x K, gated: the gate's rows then up's); tile 0 picks by size."""
+    rows, K = weight.shape
+    N = rows // 2 if gated else rows
+    if K % INT8_DEPTH != 0:
+        raise ValueError(f"int8_linear reads the {K} inputs {INT8_DEPTH} at a time")
+    if x.shape[-1] != K:
+        raise ValueError(f"int8_linear: x has {x.shape[-1]} inputs and the weight {K}")
+    for tensor, dtype, name in ((x, torch.int8, "x"), (weight, torch.int8, "weight"), (x_scale, torch.float32, "x_scale"),
+                                (weight_scale, torch.float32, "weight_scale"), (bias, torch.float16, "bias"), (residual, torch.float16, "residual"),
+                                (original, torch.float16, "original"), (residual_scale, torch.float16, "residual_scale"),
+                                (input_scale, torch.float16, "input_scale")):
+        _require(tensor, dtype, name)
+    if out_dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"int8_linear writes fp16 or bf16, not {out_dtype}")
+    library = library_for(x.device)
+    x, weight = aligned(x), aligned(weight)
+    M = x.numel() // K
+    if x_scale.numel() != M or weight_scale.numel() != rows:
+        raise ValueError(f"int8_linear: {x_scale.numel()} row scales for {M} rows, {weight_scale.numel()} weight scales for {rows} rows")
+    out = torch.empty(*x.shape[:-1], N, device=x.device, dtype=out_dtype)
+    residual, original = aligned(residual), aligned(original)
+    for tensor, name in ((residual, "residual"), (original, "original")):
+        if tensor is not None and tensor.numel() != M * N:
+            raise ValueError(f"int8_linear: {name} has {tensor.numel()} values, not {M} x {N}")
+    code = library.chess_int8_linear(pointer(x), pointer(x_scale.contiguous()), pointer(weight), pointer(weight_scale.contiguous()),
+                                     pointer(bias.contiguous() if bias is not None else None), pointer(residual), pointer(original),
+                                     pointer(residual_scale), pointer(input_scale), pointer(out), M, N, K, int(gated),
+                                     hip_kernels.OUT_BF16 if out_dtype == torch.bfloat16 else hip_kernels.OUT_F16, tile, stream_of(x.device))
+    check(code, "int8_linear")
+    return out
+
+
+def int8_matmul_i32(x: torch.Tensor, weight: torch.Tensor, tile: int = 0) -> torch.Tensor:
+    """The exact int32 sums x @ weight^T of int8_linear's kernel, before any epilogue."""
+    _require(x, torch.int8, "x")
+    _require(weight, torch.int8, "weight")
+    N, K = weight.shape
+    if K % INT8_DEPTH != 0 or x.shape[-1] != K:
+        raise ValueError(f"int8_matmul_i32 takes depth a multiple of {INT8_DEPTH} matching the weight's {K}, not {x.shape[-1]}")
+    library = library_for(x.device)
+    x, weight = aligned(x), aligned(weight)
+    out = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.int32)
+    check(library.chess_int8_matmul_i32(pointer(x), pointer(weight), pointer(out), x.numel() // K, N, K, tile, stream_of(x.device)),
+          "int8_matmul_i32")
+    return out
+
+
+#matmul is projection, gate_up or down, which picks the tile; original, residual_scale and input_scale make it give the next block's input
+@torch.library.custom_op("chess::int8_linear", mutates_args=())
+def int8_linear(x: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias: torch.Tensor | None,
+                residual: torch.Tensor | None, gated: bool, matmul: str, original: torch.Tensor | None = None,
+                residual_scale: torch.Tensor | None = None, input_scale: torch.Tensor | None = None) -> torch.Tensor:
+    tile = int8_tile(x.device, matmul, x.numel() // weight.shape[1])
+    return launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, original, residual_scale, input_scale, tile)
+
+
+@int8_linear.register_fake
+def _(x, x_scale, weight, weight_scale, bias, residual, gated, matmul, original=None, residual_scale=None, input_scale=None):
+    return x.new_empty(*x.shape[:-1], weight.shape[0] // 2 if gated else weight.shape[0], dtype=torch.float16)
+
+
+def launch_norm_quant(x: torch.Tensor, original: torch.Tensor | None, residual_scale: torch.Tensor | None, input_scale: torch.Tensor | None,
+                      gain: torch.Tensor, mixed: torch.Tensor | None, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    for tensor, name in ((x, "x"), (original, "original"), (residual_scale, "residual_scale"), (input_scale, "input_scale"), (gain, "gain")):
+        _require(tensor, torch.float16, name)
+    library = library_for(x.device)
+    D = x.shape[-1]
+    M = x.numel() // D
+    if gain.numel() != D:
+        raise ValueError(f"norm_quant: {gain.numel()} gains for rows of {D}")
+    q = torch.empty(x.shape, device=x.device, dtype=torch.int8)
+    scale = torch.empty(x.shape[:-1], device=x.device, dtype=torch.float32)
+    code = library.chess_norm_quant(pointer(x), pointer(original), pointer(residual_scale), pointer(input_scale), pointer(gain.contiguous()),
+                                    pointer(mixed), pointer(q), pointer(scale), M, D, float(eps), stream_of(x.device))
+    check(code, "mix_norm_quant" if original is not None else "norm_quant")
+    return q, scale
+
+
+@torch.library.custom_op("chess::norm_quant", mutates_args=())
+def norm_quant(x: torch.Tensor, gain: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    return launch_norm_quant(aligned(x), None, None, None, gain, None, eps)
+
+
+@norm_quant.register_fake
+def _(x, gain, eps):
+    return x.new_empty(x.shape, dtype=torch.int8), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+@torch.library.custom_op("chess::mix_norm_quant", mutates_args=())
+def mix_norm_quant(x: torch.Tensor, original: torch.Tensor, residual_scale: torch.Tensor, input_scale: torch.Tensor, gain: torch.Tensor,
+                   eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    x = aligned(x)
+    original = aligned(original)
+    if original.shape != x.shape:
+        raise ValueError(f"mix_norm_quant: the input {tuple(original.shape)} does not match the stream {tuple(x.shape)}")
+    mixed = torch.empty_like(x, dtype=torch.float16)
+    q, scale = launch_norm_quant(x, original, residual_scale, input_scale, gain, mixed, eps)
+    return mixed, q, scale
+
+
+@mix_norm_quant.register_fake
+def _(x, original, residual_scale, input_scale, gain, eps):
+    return x.new_empty(x.shape, dtype=torch.float16), x.new_empty(x.shape, dtype=torch.int8), x.new_empty(x.shape[:-1], dtype=torch.float32)
+
+
+# rotation matrices seen to be Sylvester's H32: the kernel computes that transform by butterflies, never reading them
+_SYLVESTER: dict[tuple[int, int], bool] = {}
+
+
+def _check_signs(signs: torch.Tensor) -> None:
+    if tuple(signs.shape) != (HADAMARD_BLOCK, HADAMARD_BLOCK):
+        raise ValueError(f"rotate_quant rotates blocks of {HADAMARD_BLOCK}, not {tuple(signs.shape)}")
+    key = (signs.data_ptr(), 0 if signs.is_inference() else signs._version)
+    if key in _SYLVESTER:
+        return
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("rotate_quant's rotation was not seen before the graph recording began (run the block once first)")
+    if not torch.equal(signs.detach().float().cpu(), hadamard(HADAMARD_BLOCK)):
+        raise ValueError("rotate_quant's kernel rotates by Sylvester's H32; these signs are another matrix")
+    _SYLVESTER[key] = True
+
+
+#h's rows times the block-diagonal Hadamard matrix, rounded to int8 width wide
+@torch.library.custom_op("chess::rotate_quant", mutates_args=())
+def rotate_quant(h: torch.Tensor, hadamard_signs: torch.Tensor, width: int) -> tuple[torch.Tensor, torch.Tensor]:
+    _require(h, torch.float16, "h")
+    _check_signs(hadamard_signs)
+    library = library_for(h.device)
+    h = aligned(h)
+    N = h.shape[-1]
+    M = h.numel() // N
+    q = torch.empty(*h.shape[:-1], width, device=h.device, dtype=torch.int8)
+    scale = torch.empty(h.shape[:-1], device=h.device, dtype=torch.float32)
+    check(library.chess_rotate_quant(pointer(h), pointer(q), pointer(scale), M, N, width, stream_of(h.device)), "rotate_quant")
+    return q, scale
+
+
+@rotate_quant.register_fake
+def _(h, hadamard_signs, width):
+    return h.new_empty(*h.shape[:-1], width, dtype=torch.int8), h.new_empty(h.shape[:-1], dtype=torch.float32)
+
+
+class Int8Block(nn.Module):
+    """model/int8_blocks.py:254-288 of the reference: a FusedBlock whose projection, gate_up and down are int8.
+    output_scale multiplies down's scales, as fp16 inference shrinks the residual stream."""
+
+    def __init__(self, block: FusedBlock, weights: dict[str, tuple[torch.Tensor, torch.Tensor]], output_scale: float):
+        super().__init__()
+        self.heads, self.kv_heads, self.dq, self.dv, self.templates_count = block.heads, block.kv_heads, block.dq, block.dv, block.templates_count
+        self.ln1, self.ln2 = block.ln1, block.ln2
+        self.residual_scale, self.input_scale = block.residual_scale, block.input_scale
+        self.q_gain, self.k_gain, self.eps = block.q_gain, block.k_gain, block.eps
+        self.projection_bias = block.projection_bias
+        #fp16: combine_heads' input would need a scale per head
+        self.combine_heads, self.combine_heads_bias = block.combine_heads, block.combine_heads_bias
+        device = block.projection.device
+        for name, (integers, scale) in weights.items():
+            self.register_buffer(name, integers.to(device).contiguous())
+            self.register_buffer(f"{name}_scale", (scale * output_scale if name == "down" else scale).to(device, torch.float32).contiguous())
+        self.register_buffer("hadamard_signs", hadamard(HADAMARD_BLOCK).to(device, torch.float16))
+        if self.hadamard_signs.is_cuda:
+            _check_signs(self.hadamard_signs)
+        #set by link_input_mixes: the next block's scales when down mixes its input, and whether this block's input comes mixed
+        self.next_scales: tuple[nn.Parameter, nn.Parameter] | None = None
+        self.input_mixed = False
+
+    def forward(self, x: torch.Tensor, templates: torch.Tensor, original_board_embed: torch.Tensor) -> torch.Tensor:
+        if self.input_mixed:
+            normed, scale = norm_quant(x, self.ln1.weight, self.ln1.eps)
+        else:
+            x, normed, scale = mix_norm_quant(x, original_board_embed, self.residual_scale, self.input_scale, self.ln1.weight, self.ln1.eps)
+        projected = int8_linear(normed, scale, self.projection, self.projection_scale, self.projection_bias, None, False, "projection")
+        attended = template_attention(projected, templates, self.q_gain, self.k_gain, self.heads, self.kv_heads, self.dq, self.dv, self.templates_count,
+                                      self.eps)
+        x = linear(attended, self.combine_heads, self.combine_heads_bias, residual=x)
+        normed, scale = norm_quant(x, self.ln2.weight, self.ln2.eps)
+        hidden = int8_linear(normed, scale, self.gate_up, self.gate_up_scale, None, None, True, "gate_up")
+        rotated, scale = rotate_quant(hidden, self.hadamard_signs, self.down.shape[1])
+        if self.next_scales is None:
+            return int8_linear(rotated, scale, self.down, self.down_scale, None, x, False, "down")
+        return int8_linear(rotated, scale, self.down, self.down_scale, None, x, False, "down", original_board_embed, *self.next_scales)
+
+
+def kernels(device: torch.device):
+    """The kernels for device, loaded and checked now rather than while a graph records (reference int8_cuda.py:334-344)."""
+    return library_for(device)
+
+
+def quantize_blocks(model: nn.Module, weights: dict[int, dict], output_scale: float) -> nn.Module:
+    """model's blocks of the layers in weights become Int8Blocks; the input mixes are relinked (reference int8_blocks.py:292-298)."""
+    blocks = [Int8Block(block, weights[layer], output_scale) if layer in weights else block for layer, block in enumerate(model.encoder)]
+    link_input_mixes(blocks)
+    model.encoder = nn.ModuleList(blocks)
+    if weights:
+        kernels(next(model.parameters()).device)
+    return model

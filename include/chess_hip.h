@@ -1,0 +1,86 @@
+/* C ABI of libchess_hip.so: the gfx950 kernels of Fry's int8 network evaluation.
+ *
+ * Every entry point takes plain device pointers and sizes plus the hipStream_t to launch on (as
+ * void*), launches asynchronously, allocates nothing and returns 0, a hipError_t (below 1000), or
+ * one of the CHESS_* codes; chess_last_error() then describes the argument that was refused.
+ * Unused optional pointers are NULL. fp16 data is IEEE binary16, scales are f32.
+ *
+ * The reference launches its kernels through ctypes (cuLaunchKernelEx on NVRTC modules,
+ * model/int8_cuda.py:288-327, model/attention_cuda.py:346-391) or Triton; these entry points take
+ * that place, keeping the pointer order of the reference's kernels.
+ */
+#ifndef CHESS_HIP_H
+#define CHESS_HIP_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CHESS_INVALID_SHAPE 1001 /* a size or pointer the operator cannot take (Python: ValueError) */
+#define CHESS_MISALIGNED 1002    /* an operand not 16-byte aligned (Python: ValueError) */
+#define CHESS_UNSUPPORTED 1003   /* a shape outside what the kernels were built for (Python: ValueError) */
+
+#define CHESS_OUT_F16 0
+#define CHESS_OUT_BF16 1
+#define CHESS_OUT_F32 2
+
+/* RMSNorm with gain, then per-row symmetric int8: q[M, D], scale[M] = absmax / 127.
+ * With original != NULL it first stores mixed = fp16(x * residual_scale + original * input_scale)
+ * and normalises that. Replaces model/int8_blocks.py:156-188 (norm_quant_kernel, launch_norm_quant),
+ * behind the ops norm_quant (:191-198) and mix_norm_quant (:201-212). */
+int chess_norm_quant(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain,
+                     void* mixed, void* q, void* scale, int M, int D, float eps, void* stream);
+
+/* h[M, N] fp16 zero-padded to width, each 32-column block times Sylvester's H32, then per-row int8:
+ * q[M, width], scale[M]. Replaces model/int8_blocks.py:216-246 (rotate_quant_kernel, op rotate_quant). */
+int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int width, void* stream);
+
+/* out[M, N] = epilogue(x[M, K] @ w[N(x2 if gated), K]^T) with x, w int8 and exact int32 sums;
+ * epilogue: dequantise by x_scale[M] and w_scale[N(x2)], + bias[N], silu(gate) * up when gated,
+ * + residual[M, N], then the next block's input mix when original != NULL; fp16 or bf16 out.
+ * K % 64 == 0. tile: 0 picks by size, 1 forces 64-row tiles, 2 128-row tiles; no tile changes a bit.
+ * Pointer order of small_int8 (model/int8_cuda.py:35-39); replaces int8_linear_kernel
+ * and small_int8 (model/int8_blocks.py:66-144, model/int8_cuda.py:34-183, :362-383). */
+int chess_int8_linear(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* bias, const void* residual,
+                      const void* original, const void* residual_scale, const void* input_scale, void* out, int M, int N, int K,
+                      int gated, int out_dtype, int tile, void* stream);
+
+/* The raw int32 sums out[M, N] = x[M, K] @ w[N, K]^T of the same kernel, for checking them to the bit
+ * (the reference reads them only through its epilogue: model/int8_blocks.py:85-97). */
+int chess_int8_matmul_i32(const void* x, const void* w, void* out, int M, int N, int K, int tile, void* stream);
+
+/* Template attention of B positions of T tokens (64 <= T <= 128): projected[B, T, H*dq | KV*dq | KV*dv | H*tc]
+ * fp16, templates[tc, 64, 64] fp16, q_gain/k_gain[dq] fp16 -> out[B, T, H*dv] fp16; scale = 1/sqrt(dq).
+ * groups_per_block key/value groups share a workgroup (any divisor of KV; it changes no bit).
+ * Replaces template_attention_cuda (model/attention_cuda.py:97-304, launch :379-391, pointer order
+ * projected, templates, q_gain, k_gain, out) and the Triton pair template_bias_kernel +
+ * template_attention_kernel (model/fused_blocks.py:35-171). */
+int chess_template_attention(const void* projected, const void* templates, const void* q_gain, const void* k_gain, void* out, int B,
+                             int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block, float eps,
+                             float scale, void* stream);
+
+/* out[M, N] = epilogue(x[M, K] @ w[K, N(x2 if gated)]), x and w fp16 (w in_features x out_features),
+ * f32 sums; epilogue + bias, silu(gate) * up, + residual, input mix as chess_int8_linear; fp16 or f32
+ * (accumulate_fp32) out. K % 32 == 0, N % 8 == 0. Replaces linear_kernel / launch_linear
+ * (model/fused_blocks.py:229-304) behind the op linear (:308-318). */
+int chess_linear(const void* x, const void* w, const void* bias, const void* residual, const void* original, const void* residual_scale,
+                 const void* input_scale, void* out, int M, int N, int K, int gated, int out_dtype, int tile, void* stream);
+
+/* Fills table[0..6] with hipSetDevice, hipMemcpyAsync, hipGraphLaunch, hipEventRecord, hipEventSynchronize,
+ * hipStreamSynchronize, hipGetErrorString: the address table of engine/cuda_runtime.py:17-49 (CudaRuntime.CALLS
+ * and addresses()), whose HIP functions have the CUDA ones' signatures; the native round loop
+ * (engine/selfplay_rs/src/rounds.rs:19-56) calls them by address. */
+int chess_runtime_addresses(void** table, int count);
+
+/* A description of a code, and the message of the last refused call on this thread. */
+const char* chess_error_string(int code);
+const char* chess_last_error(void);
+
+/* The GPU target the library was built for ("gfx950"). */
+const char* chess_target(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

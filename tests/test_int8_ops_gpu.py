@@ -1,0 +1,348 @@
+"""Parity of the HIP operators with the CPU oracle, on the GPU.
+
+Integer and quantised outputs are checked to the bit (int32 sums, int8 activations and their scales,
+and the fp16/bf16 outputs of every epilogue but the gated one); float outputs at the tolerances the
+reference's own tests use (tests/test_int8.py:76-90, 246-281 and tests/test_attention_cuda.py:51-71 of
+the reference)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import int8_ops as oracle
+from model import fused_blocks, int8_blocks
+from model.int8_blocks import (HADAMARD_BLOCK, INT8_TILES, hadamard, int8_linear, int8_matmul_i32, launch_int8_linear, mix_norm_quant,
+                               norm_quant, rotate_quant)
+from model.fused_blocks import launch_linear, launch_template_attention, linear, template_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def cpu(tensor: torch.Tensor) -> np.ndarray:
+    return tensor.detach().cpu().numpy()
+
+
+def bits_equal(found: torch.Tensor, expected: np.ndarray) -> bool:
+    found = cpu(found)
+    return found.shape == expected.shape and np.array_equal(found.view(np.uint8), np.ascontiguousarray(expected.astype(found.dtype)).view(np.uint8))
+
+
+@pytest.mark.parametrize("D", [128, 192, 256, 512, 768])
+@pytest.mark.parametrize("mix", [False, True])
+def test_norm_quant_matches_the_oracle_to_the_bit(device, D, mix):
+    torch.manual_seed(D)
+    x = (torch.randn(3, 70, D, device=device) * 4).half()
+    original = torch.randn(3, 70, D, device=device).half()
+    gain = (torch.rand(D, device=device) + 0.5).half()
+    rs, is_ = torch.tensor([0.8], device=device).half(), torch.tensor([0.5], device=device).half()
+    if mix:
+        mixed, q, scale = mix_norm_quant(x, original, rs, is_, gain, 1e-5)
+        expected_mixed, expected_q, expected_scale = oracle.mix_norm_quant(cpu(x), cpu(original), cpu(rs), cpu(is_), cpu(gain), 1e-5)
+        assert bits_equal(mixed, expected_mixed)
+    else:
+        q, scale = norm_quant(x, gain, 1e-5)
+        expected_q, expected_scale = oracle.norm_quant(cpu(x), cpu(gain), 1e-5)
+    assert q.dtype == torch.int8 and scale.dtype == torch.float32
+    assert bits_equal(q, expected_q) and bits_equal(scale, expected_scale)
+
+
+def test_norm_quant_rounds_the_rmsnorm(device):
+    """The reference's own check (tests/test_int8.py:246-264): the scale is absmax / 127 of torch's rms_norm, every value
+    within 0.501 of a step."""
+    torch.manual_seed(0)
+    x, original = torch.randn(2, 70, 192, device=device).half() * 4, torch.randn(2, 70, 192, device=device).half()
+    gain = (torch.rand(192, device=device) + 0.5).half()
+    residual_scale, input_scale = torch.tensor([0.8], device=device).half(), torch.tensor([0.5], device=device).half()
+    for mix in (False, True):
+        if mix:
+            mixed, integers, scale = mix_norm_quant(x, original, residual_scale, input_scale, gain, 1e-5)
+            assert mixed.dtype == torch.float16 and torch.allclose(mixed.float(), 0.8 * x.float() + 0.5 * original.float(), atol=4e-3, rtol=1e-3)
+            normed = F.rms_norm(mixed.float(), (192,), gain.float(), 1e-5)
+        else:
+            integers, scale = norm_quant(x, gain, 1e-5)
+            normed = F.rms_norm(x.float(), (192,), gain.float(), 1e-5)
+        step = normed.abs().amax(dim=-1) / 127
+        assert integers.dtype == torch.int8 and torch.allclose(scale, step, rtol=1e-5)
+        assert ((integers.float() * scale[..., None] - normed).abs() <= 0.501 * step[..., None]).all()
+
+
+@pytest.mark.parametrize("hidden, width", [(992, 1024), (320, 384), (2048, 2048), (100, 128)])
+def test_rotate_quant_matches_the_oracle_to_the_bit(device, hidden, width):
+    torch.manual_seed(hidden)
+    h = torch.randn(3, 70, hidden, device=device).half()
+    integers, scale = rotate_quant(h, hadamard(HADAMARD_BLOCK).to(device).half(), width)
+    expected_q, expected_scale = oracle.rotate_quant(cpu(h), width)
+    # a 32-block of padding alone rotates to zeros; a block that holds real columns spreads them over all 32
+    padding = -(-hidden // HADAMARD_BLOCK) * HADAMARD_BLOCK
+    assert integers.shape == (3, 70, width) and (integers[..., padding:] == 0).all()
+    assert bits_equal(integers, expected_q) and bits_equal(scale, expected_scale)
+
+
+@pytest.mark.parametrize("hidden, width", [(992, 1024), (320, 384)])
+def test_rotate_quant_rounds_the_rotated_rows(device, hidden, width):
+    """The reference's check (tests/test_int8.py:267-281) against the fp32 block-diagonal rotation."""
+    torch.manual_seed(0)
+    h = torch.randn(3, 70, hidden, device=device).half()
+    integers, scale = rotate_quant(h, hadamard(HADAMARD_BLOCK).to(device).half(), width)
+    rotation = torch.block_diag(*[hadamard(HADAMARD_BLOCK)] * (width // HADAMARD_BLOCK)).to(device)
+    rotated = F.pad(h.float(), (0, width - hidden)) @ rotation
+    step = rotated.abs().amax(dim=-1) / 127
+    assert torch.allclose(scale, step, rtol=1e-5)
+    assert ((integers.float() * scale[..., None] - rotated).abs() <= 0.501 * step[..., None]).all()
+
+
+def test_rotate_quant_refuses_another_rotation(device):
+    h = torch.randn(70, 128, device=device).half()
+    with pytest.raises(ValueError):
+        rotate_quant(h, -hadamard(HADAMARD_BLOCK).to(device).half(), 128)
+
+
+@pytest.mark.parametrize("M, N, K", [(1, 196, 256), (70, 200, 1024), (140, 1600, 512), (4480, 1536, 512), (4480, 512, 2048), (333, 64, 64)])
+@pytest.mark.parametrize("tile", [1, 2])
+def test_int8_sums_are_exact(device, M, N, K, tile):
+    generator = torch.Generator(device="cpu").manual_seed(M + N + K)
+    x = torch.randint(-127, 128, (M, K), generator=generator, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=generator, dtype=torch.int8)
+    found = int8_matmul_i32(x.to(device), w.to(device), tile)
+    expected = x.long() @ w.long().T
+    assert found.dtype == torch.int32 and torch.equal(found.cpu().long(), expected)
+
+
+def int8_operands(matmul: str, rows: int, device, width: int = 200, depth: int | None = None):
+    torch.manual_seed(rows + width)
+    down, gated = matmul.endswith("down"), matmul == "gate_up"
+    depth = depth or (1024 if down else 256)
+    x = torch.randint(-127, 128, (rows, depth), device=device, dtype=torch.int8)
+    x_scale = torch.rand(rows, device=device) / 100
+    weight = torch.randint(-127, 128, (2 * width if gated else width, depth), device=device, dtype=torch.int8)
+    weight_scale = torch.rand(len(weight), device=device) / 100
+    bias = torch.randn(width, device=device).half() if matmul == "projection" else None
+    residual = torch.randn(rows, width, device=device).half() if down else None
+    mix = (torch.randn(rows, width, device=device).half(), torch.tensor([0.9], device=device).half(),
+           torch.tensor([0.3], device=device).half()) if matmul == "mixing down" else (None, None, None)
+    return x, x_scale, weight, weight_scale, bias, residual, gated, mix
+
+
+def oracle_int8_linear(operands, out_dtype=np.float16):
+    x, x_scale, weight, weight_scale, bias, residual, gated, (original, rs, is_) = operands
+    arrays = [None if t is None else cpu(t) for t in (x, x_scale, weight, weight_scale, bias, residual, original, rs, is_)]
+    x, x_scale, weight, weight_scale, bias, residual, original, rs, is_ = arrays
+    return oracle.int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, original, rs, is_, out_dtype)
+
+
+@pytest.mark.parametrize("matmul", ["projection", "down", "mixing down"])
+@pytest.mark.parametrize("rows", [70, 210, 4480])
+def test_int8_linear_epilogues_match_the_oracle_to_the_bit(device, matmul, rows):
+    operands = int8_operands(matmul, rows, device)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    expected = oracle_int8_linear(operands)
+    for tile in (1, 2):
+        out = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
+        assert out.dtype == torch.float16 and bits_equal(out, expected), tile
+
+
+@pytest.mark.parametrize("rows", [70, 4480])
+def test_the_gated_epilogue_is_silu_times_up(device, rows):
+    operands = int8_operands("gate_up", rows, device)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    expected = oracle_int8_linear(operands).astype(np.float64)
+    first = None
+    for tile in (1, 2):
+        out = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
+        assert np.allclose(cpu(out).astype(np.float64), expected, atol=1e-3, rtol=2e-3), tile
+        first = out if first is None else first
+        assert torch.equal(out, first)
+
+
+def dequantised(integers: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    return integers.double() * scale.double()[:, None]
+
+
+@pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])
+@pytest.mark.parametrize("boards", [1, 3])
+def test_int8_linear_is_the_dequantised_matmul(device, matmul, boards):
+    """The reference's check (tests/test_int8.py:59-90): every tile, rows and columns leaving tiles part empty."""
+    torch.manual_seed(0)
+    down, gated = matmul.endswith("down"), matmul == "gate_up"
+    width, depth = 200, 1024 if down else 256
+    x = torch.randint(-127, 128, (boards, 70, depth), device=device, dtype=torch.int8)
+    x_scale = torch.rand(boards, 70, device=device) / 100
+    weight = torch.randint(-127, 128, (2 * width if gated else width, depth), device=device, dtype=torch.int8)
+    weight_scale = torch.rand(len(weight), device=device) / 100
+    bias = torch.randn(width, device=device).half() if matmul == "projection" else None
+    residual = torch.randn(boards, 70, width, device=device).half() if down else None
+    mix = (torch.randn(boards, 70, width, device=device).half(), torch.tensor(0.9, device=device).half(),
+           torch.tensor(0.3, device=device).half()) if matmul == "mixing down" else ()
+    projected = dequantised(x.reshape(-1, depth), x_scale.reshape(-1)) @ dequantised(weight, weight_scale).t()
+    if matmul == "projection":
+        expected = projected + bias.double()
+    elif matmul == "gate_up":
+        gate, up = projected.chunk(2, dim=-1)
+        expected = F.silu(gate) * up
+    else:
+        expected = projected + residual.reshape(-1, width).double()
+    if mix:
+        original, residual_scale, input_scale = mix
+        expected = residual_scale.double() * expected.half().double() + input_scale.double() * original.reshape(-1, width).double()
+    for tile in dict.fromkeys(tile for tiles in INT8_TILES.values() for _, tile in tiles["down" if down else matmul]):
+        out = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *(mix or (None, None, None)), tile)
+        assert out.dtype == torch.float16 and out.shape == (boards, 70, width)
+        assert torch.allclose(out.reshape(-1, width).double(), expected, atol=1e-3, rtol=2e-3), tile
+
+
+def test_int8_linear_writes_bf16(device):
+    operands = int8_operands("projection", 4096, device, width=1536, depth=512)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    out = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 0, torch.bfloat16)
+    expected = oracle_int8_linear(operands, "bf16")
+    assert out.dtype == torch.bfloat16
+    assert np.array_equal(cpu(out.float()), expected)
+
+
+def test_the_op_picks_a_tile_and_keeps_the_bits(device):
+    operands = int8_operands("down", 140, device)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    assert torch.equal(int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, "down"),
+                       launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 2))
+
+
+def test_int8_linear_refuses_what_it_cannot_take(device):
+    x, x_scale, weight, weight_scale, bias, *_ = int8_operands("projection", 70, device)
+    with pytest.raises(ValueError):
+        launch_int8_linear(x[:, :96].contiguous(), x_scale, weight[:, :96].contiguous(), weight_scale, bias, None, False, None, None, None)
+    with pytest.raises(ValueError):
+        launch_int8_linear(x.float(), x_scale, weight, weight_scale, bias, None, False, None, None, None)
+
+
+HEADS, KV_HEADS, DV, TEMPLATES, TOKENS, EPS = 24, 12, 32, 8, 70, 1e-5
+
+
+def attention_operands(device, positions, heads, kv_heads, dq, dv, seed=0, tokens=TOKENS, templates_count=TEMPLATES):
+    torch.manual_seed(seed)
+    projected = torch.randn(positions, tokens, heads * dq + kv_heads * dq + kv_heads * dv + heads * templates_count, device=device).half()
+    templates = (torch.randn(templates_count, 64, 64, device=device) / 2).half()
+    q_gain, k_gain = (1 + torch.randn(2, dq, device=device) / 10).half()
+    return projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_count, EPS
+
+
+def reference_attention(arguments):
+    """The reference's fp32 formula (tests/test_attention_cuda.py:51-60)."""
+    projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_count, eps = arguments
+    B, T, _ = projected.shape
+    q, k, v, c = projected.float().split([heads * dq, kv_heads * dq, kv_heads * dv, heads * templates_count], dim=-1)
+    q = F.rms_norm(q.reshape(B, T, heads, dq), (dq,), q_gain.float(), eps).transpose(1, 2)
+    k = F.rms_norm(k.reshape(B, T, kv_heads, dq), (dq,), k_gain.float(), eps).transpose(1, 2).repeat_interleave(heads // kv_heads, 1)
+    v = v.reshape(B, T, kv_heads, dv).transpose(1, 2).repeat_interleave(heads // kv_heads, 1)
+    bias = torch.einsum("biht,tij->bhij", c[:, :64].reshape(B, 64, heads, templates_count), templates.float())
+    scores = q @ k.transpose(-2, -1).contiguous() / math.sqrt(dq) + F.pad(bias, (0, T - 64, 0, T - 64))
+    return (torch.softmax(scores, -1) @ v).transpose(1, 2).reshape(B, T, heads * dv)
+
+
+ATTENTION_SHAPES = [(24, 12, 8, 32), (24, 12, 16, 32), (24, 12, 24, 32), (8, 8, 64, 64), (4, 2, 16, 32), (8, 8, 32, 32)]
+
+
+@pytest.mark.parametrize("heads, kv_heads, dq, dv", ATTENTION_SHAPES)
+@pytest.mark.parametrize("positions", [1, 5, 37])
+def test_template_attention_is_the_attention_in_fp32(device, heads, kv_heads, dq, dv, positions):
+    arguments = attention_operands(device, positions, heads, kv_heads, dq, dv)
+    out = template_attention(*arguments)
+    expected = reference_attention(arguments)
+    assert out.dtype == torch.float16 and out.shape == expected.shape
+    assert torch.allclose(out.float(), expected, atol=1e-2)
+    rounded = oracle.template_attention(*(cpu(t) if isinstance(t, torch.Tensor) else t for t in arguments))
+    assert np.abs(cpu(out.float()) - rounded).max() < 4e-3
+
+
+def test_template_attention_at_64_tokens_with_a_bias_per_head(device):
+    """BASELINE config 2's case, per-head bias: templates_count = heads and one-hot coefficients."""
+    projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps = attention_operands(device, 16, 8, 8, 64, 64, tokens=64)
+    c = projected[..., -heads * count:].reshape(16, 64, heads, count)
+    c.zero_()
+    c[..., torch.arange(heads), torch.arange(heads)] = 1.0
+    arguments = (projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps)
+    out = template_attention(*arguments)
+    assert torch.allclose(out.float(), reference_attention(arguments), atol=1e-2)
+
+
+def test_template_attention_reads_the_templates_and_their_coefficients(device):
+    """The reference's check (tests/test_attention_cuda.py:100-107)."""
+    projected, templates, *rest = attention_operands(device, 8, 24, 12, 16, 32)
+    without_bias = template_attention(projected, torch.zeros_like(templates), *rest)
+    mixed = projected.clone()
+    mixed[..., -HEADS * TEMPLATES:] = 0
+    assert torch.equal(without_bias, template_attention(mixed, templates, *rest))
+    assert (template_attention(projected, templates, *rest).float() - without_bias.float()).abs().max() > 0.05
+
+
+def test_groups_a_workgroup_change_no_bit(device):
+    arguments = attention_operands(device, 9, 8, 4, 32, 32, seed=3)
+    found = [launch_template_attention(*arguments, groups_per_block=groups) for groups in (1, 2, 4)]
+    assert all(torch.equal(found[0], other) for other in found[1:])
+
+
+def test_template_attention_refuses_what_it_cannot_take(device):
+    projected, templates, q_gain, k_gain, *rest = attention_operands(device, 2, 8, 8, 64, 64)
+    with pytest.raises(ValueError):
+        template_attention(projected.float(), templates, q_gain, k_gain, *rest)
+    with pytest.raises(ValueError):
+        template_attention(projected[:, :, :-8], templates, q_gain, k_gain, *rest)
+
+
+@pytest.mark.parametrize("M, K, N", [(70, 512, 512), (4480, 512, 512), (210, 768, 1600), (333, 96, 40)])
+def test_linear_is_the_matmul(device, M, K, N):
+    torch.manual_seed(M)
+    x = torch.randn(M, K, device=device).half()
+    weight = (torch.randn(K, N, device=device) / math.sqrt(K)).half()
+    bias, residual = torch.randn(N, device=device).half(), torch.randn(M, N, device=device).half()
+    expected = oracle.linear(cpu(x), cpu(weight), cpu(bias), cpu(residual)).astype(np.float64)
+    for tile in (1, 2):
+        out = launch_linear(x, weight, bias, residual, False, False, None, None, None, tile)
+        assert out.dtype == torch.float16 and np.allclose(cpu(out).astype(np.float64), expected, atol=2e-3, rtol=2e-3), tile
+
+
+def test_linear_gated_mixed_and_fp32(device):
+    torch.manual_seed(1)
+    x = torch.randn(280, 256, device=device).half()
+    gate_up = (torch.randn(256, 2 * 320, device=device) / 16).half()
+    hidden = linear(x, gate_up, gated=True)
+    expected = oracle.linear(cpu(x), cpu(gate_up), gated=True).astype(np.float64)
+    assert np.allclose(cpu(hidden).astype(np.float64), expected, atol=2e-3, rtol=4e-3)
+    down = (torch.randn(320, 256, device=device) / 18).half()
+    residual, original = torch.randn(280, 256, device=device).half(), torch.randn(280, 256, device=device).half()
+    rs, is_ = torch.tensor([0.8], device=device).half(), torch.tensor([0.5], device=device).half()
+    mixed = linear(hidden, down, residual=residual, original=original, residual_scale=rs, input_scale=is_)
+    expected = oracle.linear(cpu(hidden), cpu(down), residual=cpu(residual), original=cpu(original), residual_scale=cpu(rs),
+                             input_scale=cpu(is_)).astype(np.float64)
+    assert np.allclose(cpu(mixed).astype(np.float64), expected, atol=4e-3, rtol=4e-3)
+    wide = linear(x, gate_up, accumulate_fp32=True)
+    assert wide.dtype == torch.float32
+    assert np.allclose(cpu(wide), cpu(x).astype(np.float64) @ cpu(gate_up).astype(np.float64), atol=1e-3, rtol=1e-4)
+
+
+def test_the_kernels_run_in_graphs_on_two_streams(device):
+    """The reference's isolation check (tests/test_int8.py:161-184, tests/test_attention_cuda.py:110-130): two graphs replayed
+    together on two streams give the eager bits."""
+    operands = int8_operands("mixing down", 140, device)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    attention = attention_operands(device, 6, 24, 12, 24, 32, seed=2)
+    signs = hadamard(HADAMARD_BLOCK).to(device).half()
+    run = lambda first: (int8_linear(first, x_scale, weight, weight_scale, bias, residual, gated, "down", *mix),
+                         template_attention(*attention), rotate_quant(residual, signs, 256)[0])
+    inputs = [x, x.flip(0).contiguous()]
+    expected = [run(first) for first in inputs]
+    streams, buffers, graphs, outputs = [torch.cuda.Stream() for _ in range(2)], [first.clone() for first in inputs], [], []
+    for stream, buffer in zip(streams, buffers):
+        stream.wait_stream(torch.cuda.current_stream())
+        graphs.append(torch.cuda.CUDAGraph())
+        with torch.cuda.graph(graphs[-1], stream=stream):
+            outputs.append(run(buffer))
+    for replay in range(5):
+        torch.cuda.synchronize()
+        for stream, graph in zip(streams, graphs):
+            with torch.cuda.stream(stream):
+                graph.replay()
+        torch.cuda.synchronize()
+        for found, answer in zip(outputs, expected):
+            assert all(torch.equal(a, b) for a, b in zip(found, answer)), replay
