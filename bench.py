@@ -1,0 +1,291 @@
+"""Benchmark of Fry's int8 network evaluation on one MI355X.
+
+A step is one forward of the 28-block d512 int8 network (27 int8 blocks + the fp16 last, the reference's semantics at
+BASELINE's sizes) over a batch of synthetic positions already on the GPU, replayed as a HIP graph as the engine's lanes
+replay theirs. Prints ONE JSON line: positions/s at batch 1024 (value), batch-64 latency, the standalone GEMM and
+attention configs, the roofline of the dominant kernel (timed with HIP events on the stream it runs on) and the CPU
+baseline (the CPU oracle's fp32 forward, the reference's CPU path, on a bounded sample, on this host's cores).
+
+python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024] [--sweep] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _path in (ROOT, ROOT / "chess-transformer_amd"):
+    if str(_path) not in sys.path:
+        sys.path.insert(0, str(_path))
+
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA, TOPS
+FP16_PEAK_TFLOPS = 2500.0    # dense fp16/bf16 MFMA
+HBM_PEAK_GBS = 8000.0
+SETTINGS = {"d_model": 512, "num_layers": 28, "n_heads": 8, "kv_heads": 8, "mlp_hidden": 2048, "value_bins": 128, "position_templates": 8}
+TOKENS = 70
+
+
+def log(message: str) -> None:
+    print(message, file=sys.stderr, flush=True)
+
+
+def synthetic_model(settings: dict, seed: int = 0):
+    """Random-init weights as BASELINE states them: linear weights and biases N(0, 0.02), norm gains 1 + N(0, 0.1), templates
+    N(0, 0.5), square-feature table N(0, 0.1), the input mixed in (residual 0.8, input 0.5)."""
+    import torch
+    from model.model import ChessTransformer
+    torch.manual_seed(seed)
+    model = ChessTransformer(**settings).eval()
+    with torch.no_grad():
+        for name, parameter in model.named_parameters():
+            if name.endswith("residual_scale"):
+                parameter.fill_(0.8)
+            elif name.endswith("input_scale"):
+                parameter.fill_(0.5)
+            elif name == "templates":
+                parameter.normal_(std=0.5)
+            elif name == "square_features.table":
+                parameter.normal_(std=0.1)
+            elif "norm" in name or name.startswith("ln") or ".ln" in name:
+                parameter.copy_(1 + 0.1 * torch.randn_like(parameter))
+            else:
+                parameter.normal_(std=0.02)
+    return model
+
+
+def random_boards(count: int, seed: int = 0):
+    import torch
+    generator = torch.Generator().manual_seed(seed)
+    boards = torch.randint(0, 13, (count, TOKENS), generator=generator)
+    boards[:, 64:] = torch.tensor([14, 16, 16, 16, 16, 17])
+    return boards
+
+
+class Graphed:
+    """The network recorded as one HIP graph for a batch size, replayed on its own stream."""
+
+    def __init__(self, network, batch: int, device):
+        import torch
+        self.stream = torch.cuda.Stream(device)
+        self.boards = random_boards(batch, seed=batch).to(device)
+        self.stream.wait_stream(torch.cuda.current_stream(device))
+        with torch.cuda.stream(self.stream), torch.no_grad():
+            for _ in range(2):
+                network(self.boards)
+        torch.cuda.synchronize(device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream), torch.no_grad():
+            self.outputs = network(self.boards)
+        torch.cuda.synchronize(device)
+
+    def replay(self):
+        import torch
+        with torch.cuda.stream(self.stream):
+            self.graph.replay()
+
+
+def time_graph(graphed: Graphed, steps: int, warmup: int) -> tuple[float, list[float]]:
+    """(ms per step over the timed region, per-replay ms)."""
+    import torch
+    for _ in range(warmup):
+        graphed.replay()
+    torch.cuda.synchronize()
+    events = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    start = time.perf_counter()
+    for begin, end in events:
+        begin.record(graphed.stream)
+        graphed.replay()
+        end.record(graphed.stream)
+    torch.cuda.synchronize()
+    total = (time.perf_counter() - start) * 1e3
+    return total / steps, [begin.elapsed_time(end) for begin, end in events]
+
+
+def time_kernel(launch, repeats: int = 30) -> float:
+    """Average ms of one launch, by HIP events on the current stream (the one the kernels launch on)."""
+    import torch
+    for _ in range(3):
+        launch()
+    stream = torch.cuda.current_stream()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    begin.record(stream)
+    for _ in range(repeats):
+        launch()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) / repeats
+
+
+def gemm_case(M: int, K: int, N: int, gated: bool, device, out_dtype=None, epilogue="bias"):
+    """config 1: A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02), f32 scales, bias, bf16 (or fp16) out."""
+    import torch
+    from model.int8_blocks import launch_int8_linear
+    from engine.quantization import nearest
+    generator = torch.Generator(device=device).manual_seed(M + K + N)
+    x = torch.randint(-127, 128, (M, K), device=device, dtype=torch.int8, generator=generator)
+    x_scale = torch.rand(M, device=device, generator=generator) / 100
+    weight, weight_scale = nearest(torch.randn(2 * N if gated else N, K, device=device, generator=generator) * 0.02)
+    weight, weight_scale = weight.to(device), weight_scale.to(device)
+    bias = (torch.randn(N, device=device, generator=generator) * 0.02).half() if epilogue == "bias" and not gated else None
+    out_dtype = out_dtype or torch.float16
+    return lambda: launch_int8_linear(x, x_scale, weight, weight_scale, bias, None, gated, None, None, None, 0, out_dtype)
+
+
+def gemm_bytes(M: int, K: int, N: int, gated: bool, out_bytes: int = 2) -> int:
+    rows = 2 * N if gated else N
+    return M * K + rows * K + 4 * M + 4 * rows + 2 * N + out_bytes * M * N
+
+
+def standalone_gemms(device) -> dict:
+    """the four per-layer shapes at M = 4096, 16384, 65536 with bf16 out."""
+    import torch
+    results = {}
+    for M in (4096, 16384, 65536):
+        for name, K, N in (("qkv", 512, 1536), ("attention_out", 512, 512), ("ffn_up", 512, 2048), ("ffn_down", 2048, 512)):
+            ms = time_kernel(gemm_case(M, K, N, False, device, torch.bfloat16))
+            tops = 2 * M * N * K / ms / 1e9
+            gbs = gemm_bytes(M, K, N, False) / ms / 1e6
+            attainable = min(INT8_PEAK_TOPS, 2 * M * N * K / gemm_bytes(M, K, N, False) * HBM_PEAK_GBS / 1e3)
+            results[f"{name}_M{M}"] = {"ms": round(ms, 4), "tops": round(tops, 1), "frac_of_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                                       "frac_of_attainable": round(tops / attainable, 4), "gb_per_s": round(gbs, 1)}
+    return results
+
+
+def standalone_attention(device) -> dict:
+    """4096 positions x 8 heads x 64 wide over 64 tokens, a learned 64 x 64 bias per head (one-hot template mix)."""
+    import torch
+    from model.fused_blocks import template_attention
+    B, T, H, d = 4096, 64, 8, 64
+    generator = torch.Generator(device=device).manual_seed(2)
+    projected = torch.randn(B, T, 3 * H * d + H * H, device=device, generator=generator).half()
+    mix = projected[..., 3 * H * d:].reshape(B, T, H, H)
+    mix.zero_()
+    mix[..., torch.arange(H), torch.arange(H)] = 1.0
+    templates = (torch.randn(H, 64, 64, device=device, generator=generator) * 0.5).half()
+    gains = torch.ones(d, device=device).half()
+    ms = time_kernel(lambda: template_attention(projected, templates, gains, gains, H, H, d, d, H, 1e-5))
+    moved = projected.numel() * 2 + B * T * H * d * 2 + templates.numel() * 2
+    return {"ms": round(ms, 4), "gb_per_s": round(moved / ms / 1e6, 1), "frac_of_hbm": round(moved / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "bytes": moved, "positions": B}
+
+
+def cpu_baseline(model_state: dict, sample: int) -> dict:
+    """The CPU oracle's fp32 forward (the reference's CPU path, model/model.py:245-270) on a bounded sample, this host's cores."""
+    import torch
+    from oracle import network as oracle_network
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    boards = random_boards(sample, seed=11)
+    oracle_network.fp32_forward(model_state, SETTINGS, boards[:2])
+    start = time.perf_counter()
+    oracle_network.fp32_forward(model_state, SETTINGS, boards)
+    seconds = time.perf_counter() - start
+    return {"value": round(sample / seconds, 2), "unit": "positions/s", "cores": threads, "kind": "port",
+            "sample": f"{sample} positions, one fp32 forward of the d512 x 28 network (oracle/network.py fp32_forward, torch CPU), {seconds:.1f} s"}
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=5)
+    parser.add_argument("--batch", type=int, default=1024)
+    parser.add_argument("--latency-batch", type=int, default=64)
+    parser.add_argument("--sweep", action="store_true", help="also time batches 1, 16, 64, 256, 1024, 4096")
+    parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    parser.add_argument("--cpu-sample", type=int, default=256)
+    parser.add_argument("--no-standalone", action="store_true", help="skip the standalone GEMM and attention configs")
+    arguments = parser.parse_args()
+    if arguments.gpus != 1:
+        print(f"bench.py measures one GPU: every box here has one and nothing in this build uses a second (asked for {arguments.gpus})",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from engine.inference import int8_network
+    from engine.quantization import nearest_int8_weights
+    from model.int8_blocks import launch_int8_linear
+
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    log(f"building the d512 x 28 int8 network on {torch.cuda.get_device_name(device)}")
+    model = synthetic_model(SETTINGS)
+    state = {name: value.clone() for name, value in model.state_dict().items()}
+    weights = nearest_int8_weights(model)
+    network = int8_network(model.to(device), weights)
+
+    log(f"batch {arguments.batch}: recording and timing {arguments.steps} steps after {arguments.warmup} warm-up")
+    graphed = Graphed(network, arguments.batch, device)
+    ms_per_step, per_replay = time_graph(graphed, arguments.steps, arguments.warmup)
+    positions_per_s = arguments.batch / (ms_per_step / 1e3)
+    log(f"  {ms_per_step:.3f} ms/step, {positions_per_s:,.0f} positions/s")
+    del graphed
+
+    log(f"batch {arguments.latency_batch}: latency over 200 replays")
+    small = Graphed(network, arguments.latency_batch, device)
+    _, latencies = time_graph(small, 200, 20)
+    latencies.sort()
+    p50, p99 = latencies[len(latencies) // 2], latencies[int(len(latencies) * 0.99) - 1]
+    latency = {"batch": arguments.latency_batch, "p50_ms": round(p50, 4), "p99_ms": round(p99, 4),
+               "positions_per_s": round(arguments.latency_batch / (p50 / 1e3), 1)}
+    log(f"  p50 {p50:.3f} ms, p99 {p99:.3f} ms")
+    del small
+
+    sweep = {}
+    if arguments.sweep:
+        for batch in (1, 16, 64, 256, 1024, 4096):
+            graphed = Graphed(network, batch, device)
+            ms, replays = time_graph(graphed, 20, 3)
+            replays.sort()
+            sweep[batch] = {"ms_per_batch": round(ms, 4), "p50_ms": round(replays[len(replays) // 2], 4), "positions_per_s": round(batch / ms * 1e3, 1)}
+            log(f"  sweep batch {batch}: {ms:.3f} ms, {batch / ms * 1e3:,.0f} positions/s")
+            del graphed
+
+    # the dominant kernel: the gated gate_up GEMM of an int8 block at the batch's rows (2 x 2048 weight rows, depth 512)
+    M = arguments.batch * TOKENS
+    block = network.encoder[0]
+    generator = torch.Generator(device=device).manual_seed(5)
+    x = torch.randint(-127, 128, (M, 512), device=device, dtype=torch.int8, generator=generator)
+    x_scale = torch.rand(M, device=device, generator=generator) / 100
+    gate_up_ms = time_kernel(lambda: launch_int8_linear(x, x_scale, block.gate_up, block.gate_up_scale, None, None, True, None, None, None))
+    gate_up_ops = 2 * M * (2 * 2048) * 512
+    achieved = gate_up_ops / gate_up_ms / 1e9
+    roofline = {"kernel": "int8_gemm_kernel<128,64,2,fp16> (gate_up, silu epilogue)", "bound": "mfma", "achieved": round(achieved, 1),
+                "peak": INT8_PEAK_TOPS, "unit": "TOPS", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
+                "ops_per_launch": gate_up_ops, "avg_launch_ms": round(gate_up_ms, 4), "rows": M}
+    log(f"gate_up GEMM: {gate_up_ms:.3f} ms, {achieved:.0f} TOPS ({achieved / INT8_PEAK_TOPS:.1%} of dense int8 peak)")
+    del x, x_scale
+
+    standalone = {}
+    if not arguments.no_standalone:
+        standalone["gemm"] = standalone_gemms(device)
+        standalone["attention"] = standalone_attention(device)
+        log(f"standalone attention: {standalone['attention']['ms']} ms, {standalone['attention']['gb_per_s']} GB/s")
+
+    baseline = None
+    if not arguments.no_cpu:
+        log(f"CPU baseline: fp32 forward of {arguments.cpu_sample} positions")
+        baseline = cpu_baseline(state, arguments.cpu_sample)
+        log(f"  {baseline['value']} positions/s on {baseline['cores']} threads")
+
+    result = {"metric": "positions/sec at batch 1024 (28L int8 net)", "value": round(positions_per_s, 1), "unit": "positions/s", "n_gpus": 1,
+              "steps": arguments.steps, "warmup": arguments.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+              "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+              "data": "synthetic: random-init weights (N(0, 0.02)), round-to-nearest int8 per channel, random token boards",
+              "config": {"workload": f"Fry int8 network d512 x 28 (27 int8 blocks + fp16 last), T=70, batch {arguments.batch}, HIP graph replay",
+                         "batch": arguments.batch, "tokens": TOKENS, "d_model": 512, "layers": 28, "heads": 8, "mlp_hidden": 2048},
+              "batch64": latency, "roofline": roofline, "cpu_baseline": baseline, **standalone}
+    if sweep:
+        result["sweep"] = sweep
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

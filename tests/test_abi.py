@@ -1,0 +1,94 @@
+"""The C ABI of libchess_hip.so, without a GPU: every declared entry point is exported, the Python loader's argument types
+match the header, and refused arguments come back as codes with a message before anything is launched."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from model import hip_kernels
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "chess_hip.h"
+
+
+def declarations() -> dict[str, list[str]]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    found = {}
+    for name, arguments in re.findall(r"\b(chess_\w+)\s*\(([^;]*?)\)\s*;", text):
+        arguments = " ".join(arguments.split())
+        found[name] = [] if arguments in ("", "void") else [argument.strip() for argument in arguments.split(",")]
+    return found
+
+
+@pytest.fixture(scope="module")
+def library():
+    return hip_kernels.load_library()
+
+
+def test_the_library_exports_every_declared_entry_point(library):
+    names = declarations()
+    assert len(names) >= 10
+    for name in names:
+        assert getattr(library, name) is not None, name
+
+
+def test_the_loaders_argument_types_are_the_headers(library):
+    for name, arguments in declarations().items():
+        expected = []
+        for argument in arguments:
+            kind = argument.rsplit(" ", 1)[0] if " " in argument else argument
+            expected.append(ctypes.c_void_p if "*" in argument else ctypes.c_float if kind.endswith("float") else ctypes.c_int)
+        declared = hip_kernels.SIGNATURES[name]
+        normalised = [ctypes.c_void_p if t is not ctypes.c_int and t is not ctypes.c_float else t for t in declared]
+        assert normalised == expected, name
+
+
+def test_the_library_is_built_for_gfx950(library):
+    assert library.chess_target() == b"gfx950"
+
+
+MISALIGNED = 8  # never dereferenced: the checks refuse it first
+
+
+def test_refused_shapes_come_back_as_codes(library):
+    assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, -1, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    assert b"rows" in library.chess_last_error()
+    assert library.chess_norm_quant(MISALIGNED, None, None, None, 16, None, 16, 16, 4, 64, 1e-5, None) == hip_kernels.MISALIGNED
+    assert library.chess_rotate_quant(16, 16, 16, 4, 100, 100, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 100, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
+    assert b"64 at a time" in library.chess_last_error()
+    assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 7, 0, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_int8_linear(16, 16, 16, 16, None, None, 16, None, None, 16, 4, 8, 64, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_int8_matmul_i32(MISALIGNED, 16, 16, 4, 8, 64, 0, None) == hip_kernels.MISALIGNED
+    assert library.chess_int8_matmul_i32(16, 16, 16, 4, 8, 64, 3, None) == hip_kernels.UNSUPPORTED
+    attention = lambda *shape: library.chess_template_attention(16, 16, 16, 16, 16, *shape, 1e-5, 0.125, None)
+    assert attention(1, 32, 8, 8, 64, 64, 8, 1) == hip_kernels.UNSUPPORTED            # fewer than 64 tokens
+    assert attention(1, 70, 8, 3, 64, 64, 8, 1) == hip_kernels.INVALID_SHAPE           # 3 key/value heads for 8
+    assert attention(1, 70, 8, 8, 12, 64, 8, 1) == hip_kernels.UNSUPPORTED             # query width not a multiple of 8
+    assert attention(1, 70, 8, 8, 64, 48, 8, 1) == hip_kernels.UNSUPPORTED             # value width
+    assert attention(1, 70, 8, 8, 64, 64, 9, 1) == hip_kernels.UNSUPPORTED             # 9 templates
+    assert attention(1, 70, 8, 8, 64, 64, 8, 3) == hip_kernels.INVALID_SHAPE           # 3 groups a workgroup for 8
+    assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 12, 64, 0, 0, 0, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
+
+
+def test_empty_batches_launch_nothing(library):
+    assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
+    assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
+
+
+def test_codes_become_value_errors_with_the_message(library):
+    library.chess_rotate_quant(16, 16, 16, 4, 100, 100, None)
+    with pytest.raises(ValueError, match="width divisible by 32"):
+        hip_kernels.check(hip_kernels.INVALID_SHAPE, "rotate_quant")
+    with pytest.raises(RuntimeError, match="HIP error"):
+        hip_kernels.check(1, "launch")
+
+
+def test_the_runtime_table_has_the_reference_calls(library):
+    table = (ctypes.c_void_p * 7)()
+    assert library.chess_runtime_addresses(table, 7) == 0 and all(table)
+    assert len(set(table)) == 7
+    assert library.chess_runtime_addresses(table, 3) == hip_kernels.INVALID_SHAPE
+    assert library.chess_error_string(1002) == b"misaligned operand"

@@ -1,0 +1,269 @@
+"""The int8 network on the GPU against the reference's bars (tests/test_int8.py:359-457 of the reference) and the CPU oracle."""
+import copy
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from oracle import int8_ops as oracle
+from oracle import network as oracle_network
+from engine import quantization
+from engine.inference import FP16_RESIDUAL_SCALE, answer_rows, fp16_model, int8_model, int8_network
+from engine.quantization import nearest_int8_weights
+from model import fused_blocks, int8_blocks
+from model.checkpoint import save_checkpoint
+from model.fused_blocks import FusedBlock, template_attention, linear
+from model.int8_blocks import Int8Block, int8_linear, mix_norm_quant, norm_quant, rotate_quant
+from model.model import ChessTransformer, expected_score
+
+pytestmark = pytest.mark.gpu
+
+SMALL = {"d_model": 128, "num_layers": 3, "n_heads": 4, "kv_heads": 2, "qk_ratio": [0.25, 0.5, 0.75], "mlp_hidden": 320, "value_bins": 16}
+# BASELINE's configs 3/4 under the reference's semantics: d512, 28 blocks, 8 heads, SwiGLU 2048
+FULL = {"d_model": 512, "num_layers": 28, "n_heads": 8, "mlp_hidden": 2048, "value_bins": 128}
+
+
+def deeper(layers: int) -> dict:
+    ratios = SMALL["qk_ratio"]
+    return {**SMALL, "num_layers": layers, "qk_ratio": [ratios[layer % len(ratios)] for layer in range(layers)]}
+
+
+def random_boards(count: int, seed: int = 0) -> torch.Tensor:
+    """Token boards with every piece code on the squares (the network's arithmetic does not need legal positions)."""
+    generator = torch.Generator().manual_seed(seed)
+    boards = torch.randint(0, 13, (count, 70), generator=generator)
+    boards[:, 64:] = torch.tensor([14, 16, 16, 16, 16, 17])
+    return boards
+
+
+def make_model(settings: dict = SMALL, seed: int = 0) -> ChessTransformer:
+    """The reference's small_checkpoint (tests/test_int8.py:312-326): the input mixed in, templates and features live, sharp priors."""
+    torch.manual_seed(seed)
+    model = ChessTransformer(**settings).eval()
+    with torch.no_grad():
+        for block in model.encoder:
+            block.residual_scale.fill_(0.8)
+            block.input_scale.fill_(0.5)
+        model.templates.normal_()
+        model.square_features.table.normal_(std=0.1)
+        model.from_projection.weight.mul_(8)
+    return model
+
+
+@pytest.fixture
+def small_calibration(monkeypatch, tmp_path):
+    monkeypatch.setattr(quantization, "CACHE", tmp_path / "cache")
+    monkeypatch.setattr(quantization, "CALIBRATION_POSITIONS", 64)
+
+
+def checkpoint(tmp_path, settings=SMALL, model=None):
+    model = model or make_model(settings)
+    save_checkpoint(model, settings, tmp_path / "model.pt")
+    return model, tmp_path / "model.pt"
+
+
+def distance(found: torch.Tensor, expected_logits: torch.Tensor) -> torch.Tensor:
+    return 0.5 * (torch.softmax(found.float(), dim=-1) - torch.softmax(expected_logits.float(), dim=-1)).abs().sum(dim=-1)
+
+
+def test_the_int8_model_computes_what_the_model_does(tmp_path, small_calibration, device):
+    model, path = checkpoint(tmp_path)
+    boards = random_boards(16)
+    with torch.no_grad():
+        expected_logits, expected_values = model(boards)
+        int8 = int8_model(path, 0, quantization.int8_weights(path, 0, boards))
+        rows = answer_rows(int8(boards.to(device))).cpu()
+        fp16_rows = answer_rows(fp16_model(path)(boards.to(device))).cpu()
+    assert [isinstance(block, Int8Block) for block in int8.encoder] == [True, True, False]
+    assert distance(rows[:, :-1], expected_logits).max() < 0.005
+    assert distance(fp16_rows[:, :-1], expected_logits).max() < distance(rows[:, :-1], expected_logits).max()
+    assert torch.equal(rows[:, :-1].argmax(-1), expected_logits.argmax(-1))
+    assert torch.allclose(rows[:, -1], expected_score(expected_values), atol=5e-3)
+
+
+def compare_with_oracle(model: ChessTransformer, settings: dict, boards: torch.Tensor, device, weights=None):
+    weights = weights or nearest_int8_weights(model)
+    state = {name: value.clone() for name, value in model.state_dict().items()}
+    network = int8_network(copy.deepcopy(model).to(device), weights)
+    with torch.no_grad():
+        logits, values = network(boards.to(device))
+    expected_logits, expected_values = oracle_network.int8_forward(state, settings, weights, boards)
+    logits, values = logits.float().cpu(), values.float().cpu()
+    assert (logits - expected_logits).abs().max() < 2e-2
+    assert (expected_score(values) - expected_score(expected_values)).abs().max() < 5e-3
+    agree = (logits.argmax(-1) == expected_logits.argmax(-1)).float().mean()
+    assert agree >= 0.999
+    return network
+
+
+def test_the_int8_network_is_the_oracles(device):
+    compare_with_oracle(make_model(), SMALL, random_boards(12, seed=1), device)
+
+
+def test_the_full_size_network_is_the_oracles(device):
+    """BASELINE's d512 x 28 network (27 int8 blocks and the fp16 last) on a few positions."""
+    model = make_model(FULL, seed=3)
+    compare_with_oracle(model, FULL, random_boards(2, seed=3), device)
+
+
+def test_down_mixes_the_next_blocks_input_to_the_bit(device):
+    network = int8_network(make_model().to(device), nearest_int8_weights(make_model()))
+    boards = random_boards(8, seed=2).to(device)
+    with torch.no_grad():
+        mixed_in_down = answer_rows(network(boards))
+        linked = [block.input_mixed for block in network.encoder[:2]]
+        for block in network.encoder[:2]:
+            block.next_scales, block.input_mixed = None, False
+        mixed_by_each = answer_rows(network(boards))
+    assert linked == [False, True] and torch.equal(mixed_in_down, mixed_by_each)
+
+
+def test_tiles_change_no_answer(device, monkeypatch):
+    network = int8_network(make_model().to(device), nearest_int8_weights(make_model()))
+    with torch.no_grad():
+        answers = [answer_rows(network(random_boards(size, seed=size).to(device))) for size in (1, 3, 16)]
+        for module in (fused_blocks, int8_blocks):
+            monkeypatch.setattr(module, "tile_for", lambda tiles, M, multiprocessors: tiles[-1][1])
+        forced = [answer_rows(network(random_boards(size, seed=size).to(device))) for size in (1, 3, 16)]
+    assert all(torch.equal(a, b) for a, b in zip(answers, forced))
+
+
+def test_graphs_on_two_streams_replay_the_eager_answers(device):
+    """A whole forward recorded as a HIP graph per lane (the reference's GraphedBatches lanes, engine/inference.py:85-130)."""
+    network = int8_network(make_model().to(device), nearest_int8_weights(make_model()))
+    boards = [random_boards(6, seed=seed).to(device) for seed in (4, 5)]
+    with torch.no_grad():
+        expected = [answer_rows(network(b)) for b in boards]
+        streams = [torch.cuda.Stream() for _ in boards]
+        buffers = [b.clone() for b in boards]
+        for stream in streams:
+            stream.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(stream):
+                network(buffers[0])  # warm-up off the default stream
+        torch.cuda.synchronize()
+        graphs, outputs = [], []
+        for stream, buffer in zip(streams, buffers):
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=stream):
+                outputs.append(answer_rows(network(buffer)))
+            graphs.append(graph)
+        for order in (1, -1):
+            for buffer, b in zip(buffers, boards[::order]):
+                buffer.copy_(b)
+            torch.cuda.synchronize()
+            for _ in range(4):
+                for stream, graph in zip(streams, graphs):
+                    with torch.cuda.stream(stream):
+                        graph.replay()
+            torch.cuda.synchronize()
+            assert all(torch.equal(out, answer) for out, answer in zip(outputs, expected[::order]))
+
+
+def cpu(tensor):
+    return tensor.detach().cpu().numpy()
+
+
+def test_every_int8_step_of_a_block_is_the_oracles_to_the_bit(device):
+    """Teacher-forced: each quantising and int8 step of Int8Block.forward gets the GPU's own inputs on both sides."""
+    network = int8_network(make_model(FULL, seed=5).to(device), nearest_int8_weights(make_model(FULL, seed=5)))
+    block = network.encoder[0]
+    x = (torch.randn(4, 70, 512, device=device) / 16).half()
+    original = (torch.randn(4, 70, 512, device=device) / 16).half()
+    same = lambda found, expected: np.array_equal(cpu(found), expected)
+    with torch.no_grad():
+        mixed, q, scale = mix_norm_quant(x, original, block.residual_scale, block.input_scale, block.ln1.weight, block.eps)
+        want = oracle.mix_norm_quant(cpu(x), cpu(original), cpu(block.residual_scale), cpu(block.input_scale), cpu(block.ln1.weight), block.eps)
+        assert all(same(f, w) for f, w in zip((mixed, q, scale), want))
+        projected = int8_linear(q, scale, block.projection, block.projection_scale, block.projection_bias, None, False, "projection")
+        assert same(projected, oracle.int8_linear(cpu(q), cpu(scale), cpu(block.projection), cpu(block.projection_scale), cpu(block.projection_bias)))
+        attended = template_attention(projected, network.templates, block.q_gain, block.k_gain, block.heads, block.kv_heads, block.dq, block.dv,
+                                      block.templates_count, block.eps)
+        stream = linear(attended, block.combine_heads, block.combine_heads_bias, residual=mixed)
+        q, scale = norm_quant(stream, block.ln2.weight, block.eps)
+        want_q, want_scale = oracle.norm_quant(cpu(stream), cpu(block.ln2.weight), block.eps)
+        assert same(q, want_q) and same(scale, want_scale)
+        hidden = int8_linear(q, scale, block.gate_up, block.gate_up_scale, None, None, True, "gate_up")
+        assert np.allclose(cpu(hidden).astype(np.float64), oracle.int8_linear(cpu(q), cpu(scale), cpu(block.gate_up), cpu(block.gate_up_scale),
+                                                                             gated=True).astype(np.float64), atol=1e-3, rtol=2e-3)
+        rotated, scale = rotate_quant(hidden, block.hadamard_signs, block.down.shape[1])
+        want_q, want_scale = oracle.rotate_quant(cpu(hidden), block.down.shape[1])
+        assert same(rotated, want_q) and same(scale, want_scale)
+        scales = block.next_scales
+        out = int8_linear(rotated, scale, block.down, block.down_scale, None, stream, False, "down", original, *scales)
+        want = oracle.int8_linear(cpu(rotated), cpu(scale), cpu(block.down), cpu(block.down_scale), residual=cpu(stream), original=cpu(original),
+                                  residual_scale=cpu(scales[0]), input_scale=cpu(scales[1]))
+        assert same(out, want)
+
+
+def test_fp16_blocks_between_int8_blocks_compute_as_the_fp16_models(device):
+    """The reference's check (tests/test_int8.py:651-667): a block kept in fp16 mixes its own input."""
+    settings = deeper(5)
+    model = make_model(settings)
+    weights = {layer: matmuls for layer, matmuls in nearest_int8_weights(model).items() if layer != 2}
+    boards = random_boards(5).to(device)
+    with torch.no_grad():
+        kept = int8_network(copy.deepcopy(model).to(device), weights)
+        answers = answer_rows(kept(boards))
+        all_int8 = int8_network(copy.deepcopy(model).to(device), nearest_int8_weights(model))
+        one_by_one = fused_blocks.FusedTransformer(copy.deepcopy(model).to(device).scale_residual_stream(FP16_RESIDUAL_SCALE).half_except_heads(torch.float16))
+        blocks = [one_by_one.encoder[layer] if layer in (2, 4) else all_int8.encoder[layer] for layer in range(5)]
+        for block in blocks:
+            block.next_scales, block.input_mixed = None, False
+        one_by_one.encoder = nn.ModuleList(blocks)
+        expected = answer_rows(one_by_one(boards))
+    assert [type(block) for block in kept.encoder] == [Int8Block, Int8Block, FusedBlock, Int8Block, FusedBlock]
+    assert torch.equal(answers, expected)
+
+
+def test_the_int8_weights_are_cached_by_the_checkpoints_content(tmp_path, small_calibration):
+    """The reference's check (tests/test_int8.py:526-553), with calibration boards given."""
+    model, path = checkpoint(tmp_path)
+    boards = random_boards(64)
+    computed = quantization.int8_weights(path, 0, boards)
+    assert sorted(computed) == [0, 1] and sorted(computed[0]) == ["down", "gate_up", "projection"]
+
+    def failing(*arguments):
+        raise AssertionError("computed again")
+    original = quantization.compute_int8_weights
+    quantization.compute_int8_weights = failing
+    try:
+        cached = quantization.int8_weights(path, 0, boards)
+    finally:
+        quantization.compute_int8_weights = original
+    for layer, matmuls in computed.items():
+        for name, (integers, scale) in matmuls.items():
+            assert integers.dtype == torch.int8 and scale.dtype == torch.float32
+            assert torch.equal(cached[layer][name][0], integers) and torch.equal(cached[layer][name][1], scale)
+    quantization.cached_weights_path(path, 0).unlink()
+    again = quantization.int8_weights(path, 0, boards)
+    assert all(torch.equal(a, b) for layer in computed for name in computed[layer] for a, b in zip(computed[layer][name], again[layer][name]))
+
+
+@pytest.mark.parametrize("outlier", [2, 3])
+def test_the_block_whose_int8_costs_most_stays_in_fp16(tmp_path, small_calibration, outlier):
+    """The reference's check (tests/test_int8.py:633-648): a gate input channel 100x the others rounds badly in int8."""
+    settings = deeper(5)
+    model = make_model(settings)
+    with torch.no_grad():
+        model.encoder[outlier].mlp.gate_projection.weight[:, 0] *= 100
+    _, path = checkpoint(tmp_path, settings, model)
+    boards = random_boards(64, seed=7)
+    errors = quantization.block_errors(path, quantization.int8_weights(path, 0, boards), boards)
+    assert sorted(errors) == [0, 1, 2, 3] and max(errors, key=errors.get) == outlier
+    assert sorted(quantization.int8_weights(path, 1, boards)) == [layer for layer in range(4) if layer != outlier]
+
+
+def test_the_runtime_table_copies_and_launches(device):
+    from engine.hip_runtime import DEVICE_TO_HOST, HOST_TO_DEVICE, hip_runtime
+    runtime = hip_runtime()
+    assert sorted(runtime.addresses()) == sorted([*runtime.CALLS, runtime.ERROR_STRING])
+    host = torch.arange(256, dtype=torch.float32).pin_memory()
+    back = torch.zeros(256, dtype=torch.float32).pin_memory()
+    on_device = torch.empty(256, device=device)
+    stream = torch.cuda.Stream()
+    runtime.check(runtime.set_device(device.index), "set device")
+    runtime.check(runtime.memcpy(on_device.data_ptr(), host.data_ptr(), 1024, HOST_TO_DEVICE, stream.cuda_stream), "copy in")
+    runtime.check(runtime.memcpy(back.data_ptr(), on_device.data_ptr(), 1024, DEVICE_TO_HOST, stream.cuda_stream), "copy out")
+    runtime.check(runtime.stream_synchronize(stream.cuda_stream), "synchronize")
+    assert torch.equal(back, host)
