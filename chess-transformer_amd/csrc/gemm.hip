@@ -1,0 +1,431 @@
+// The network's GEMMs on CDNA4 MFMA, with their fused epilogues:
+//   int8: out[M, N] = epilogue(x[M, K] @ w[N, K]^T), x and w int8, exact int32 sums (v_mfma_i32_32x32x32_i8);
+//         what model/int8_blocks.py:66-144 (int8_linear_kernel) and model/int8_cuda.py:34-183 (small_int8) compute.
+//   fp16: out[M, N] = epilogue(x[M, K] @ W[K, N]), x and W fp16, f32 sums (v_mfma_f32_32x32x16_f16); what
+//         model/fused_blocks.py:229-304 (linear_kernel) computes, W taken transposed as w = W^T [N, K].
+// int8 epilogue op order (f32, one IEEE op per step, no fma):
+//   v = f32(acc) * x_scale[m];  out = v * w_scale[n]
+//   [BIAS]      out = out + bias[n]
+//   [GATED]     up = (f32(acc_up) * x_scale[m]) * w_scale[N + n];  out = silu(out) * up
+//   [RESIDUAL]  out = out + residual[m, n]
+//   [MIX]       out = (f32(round(out)) * residual_scale) + (original[m, n] * input_scale)
+//   round to fp16 / bf16 (or, for the accumulator entry point, the raw int32 sums).
+// The fp16 epilogue is the same from the f32 sums, without the scales. The int32 sums are exact in any
+// order, and every tile shape runs the same epilogue, so the tile chosen for a shape never changes a bit.
+//
+// Layout: x row-major [M, K], w row-major [N(x2 gated), K] (the gate's rows, then up's); a stage is 64 bytes
+// of K (64 int8 or 32 fp16 elements), and K must be a multiple of it.
+// A workgroup of 4 wavefronts takes a BM x BN tile of outputs (gated: BN outputs from 2 BN weight rows);
+// the wavefronts split it WAVES_M x WAVES_N into 32 x 32 MFMA fragments.
+//
+// K advances a stage at a time through a ring of STAGES stages in LDS, filled by the DMA loads
+// global_load_lds_dwordx4 (global memory straight to LDS, no registers): STAGES - 1 stages are in flight
+// while one is multiplied, and a wavefront waits (s_waitcnt vmcnt) only for the stage it is about to read.
+// A stage holds 1 KB blocks of 16 rows x 64 bytes, a DMA instruction's 64 lanes each writing 16 bytes; a
+// row's 16-byte chunk c sits at lane (row + 16 c), so the 16 lanes of an MFMA operand group read 256
+// contiguous bytes (no bank conflicts) and a DMA instruction reads 64 contiguous bytes of each of 16 rows.
+// An MFMA operand lane holds 16 consecutive bytes of one row (16 int8 or 8 fp16); which k a byte stands
+// for is the same for both operands, so the sums are the dot products whatever the hardware's k order. The
+// weights are the MFMA's first operand: a lane's results are then groups of 4 consecutive columns of one
+// row, which take their column scales and bias 16 bytes at a time.
+// The epilogue runs in two phases through LDS: the dequantised (and gated) f32 tile is staged, then read
+// back by rows, so that residual, input embedding and outputs move 16 bytes a lane with a row's columns
+// contiguous across lanes.
+#include "chess_common.h"
+
+#include <type_traits>
+
+namespace {
+
+constexpr int STAGE_K_BYTES = 64;
+constexpr int THREADS = 256;
+constexpr int BLOCK = 1024;      // bytes a DMA instruction writes: 16 rows x 64 bytes
+
+enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4 };
+
+struct Epilogue {
+    const float* x_scale;        // int8 only
+    const float* w_scale;        // int8 only
+    const half_t* bias;
+    const half_t* residual;
+    const half_t* original;
+    const half_t* residual_scale;
+    const half_t* input_scale;
+    int flags;
+};
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+#define LDS_SPACE __attribute__((address_space(3)))
+
+template <typename In> struct Mfma;
+template <> struct Mfma<int8_t> {
+    typedef v16i Acc;
+    typedef v4i Operand;
+    static DEVICE Acc step(Operand a, Operand b, Acc c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+    static DEVICE float value(Acc c, int r) { return (float)c[r]; }
+};
+template <> struct Mfma<half_t> {
+    typedef v16f Acc;
+    typedef v8h Operand;
+    static DEVICE Acc step(Operand a, Operand b, Acc c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+    static DEVICE float value(Acc c, int r) { return c[r]; }
+};
+
+DEVICE v4h quad_halves(const half_t* p) { return *reinterpret_cast<const v4h*>(p); }
+
+template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
+template <> DEVICE void store_eight<half_t>(half_t* to, const float (&v)[8]) {
+    *reinterpret_cast<v8h*>(to) = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+}
+template <> DEVICE void store_eight<bf16_t>(bf16_t* to, const float (&v)[8]) {
+    uint32_t packed[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) packed[c] = (uint32_t)bf16_from_float(v[2 * c]).bits | ((uint32_t)bf16_from_float(v[2 * c + 1]).bits << 16);
+    *reinterpret_cast<uint4*>(to) = uint4{packed[0], packed[1], packed[2], packed[3]};
+}
+template <> DEVICE void store_eight<float>(float* to, const float (&v)[8]) {
+    *reinterpret_cast<float4*>(to) = float4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<float4*>(to + 4) = float4{v[4], v[5], v[6], v[7]};
+}
+
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding)
+constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int LGKMCNT_ZERO = 0xC07F;
+
+DEVICE void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Every wavefront's DMA loads of the stage to be read have landed and every wavefront is done reading the
+// stage the next DMA overwrites. The compiler fences of __syncthreads would wait for all loads in flight.
+template <int OUTSTANDING> DEVICE void stage_barrier() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(OUTSTANDING) & ~(0xF << 8));   // and lgkmcnt(0): this wavefront's reads are done
+    bare_barrier();
+}
+
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT>
+__global__ __launch_bounds__(THREADS) void gemm_kernel(
+    const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
+{
+    static_assert(WAVES_M * WAVES_N * 64 == THREADS, "four wavefronts");
+    typedef Mfma<In> MMA;
+    constexpr bool INT8 = std::is_same<In, int8_t>::value;
+    constexpr bool RAW = std::is_same<OutT, int>::value;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+    constexpr int A_BLOCKS = BM / 16, B_BLOCKS = NB * BN / 16, BLOCKS = A_BLOCKS + B_BLOCKS;
+    constexpr int PER_WAVE = BLOCKS / 4;
+    constexpr int STAGE_BYTES = BLOCKS * BLOCK;
+    static_assert(BLOCKS % 4 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    extern __shared__ __align__(16) int8_t lds[];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const size_t row_bytes = (size_t)K * sizeof(In);
+    const int steps = (int)(row_bytes / STAGE_K_BYTES);
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int tile = xcd_local_tile(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GROUP_M = 8;
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = tile / in_group * GROUP_M;
+    const int group_rows = min(tiles_m - first_m, GROUP_M);
+    const int m0 = (first_m + tile % in_group % group_rows) * BM;
+    const int n0 = (tile % in_group / group_rows) * BN;
+
+    // this lane's source in each of the wavefront's blocks: row (lane % 16) of the block, 16-byte chunk lane / 16.
+    // Rows past M read row M - 1 and columns past N read column N - 1: their sums are never stored.
+    const int8_t* source[PER_WAVE];
+#pragma unroll
+    for (int p = 0; p < PER_WAVE; p++) {
+        const int block = wave * PER_WAVE + p;
+        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * 16 + (lane & 15);
+        const int chunk = (lane >> 4) * 16;
+        if (block < A_BLOCKS) {
+            source[p] = (const int8_t*)x + (size_t)min(m0 + row, M - 1) * row_bytes + chunk;
+        } else {
+            const int group = row / BN, col = min(n0 + row % BN, N - 1);
+            source[p] = (const int8_t*)w + ((size_t)group * N + col) * row_bytes + chunk;
+        }
+    }
+    LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
+    auto issue = [&](int step) {
+        const int k0 = min(step, steps - 1) * STAGE_K_BYTES;
+        LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int p = 0; p < PER_WAVE; p++)
+            __builtin_amdgcn_global_load_lds((const void*)(source[p] + k0), (LDS_SPACE void*)(stage + (wave * PER_WAVE + p) * BLOCK), 16, 0, 0);
+    };
+
+    typename MMA::Acc acc[NB][FM][FN];
+#pragma unroll
+    for (int g = 0; g < NB; g++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) acc[g][i][j][r] = 0;
+
+    // an operand lane (row lane % 32, 16-byte half lane / 32) in a stage: the block of its 16 rows, then row + 16 chunk
+    const int in_row = lane & 31, half = lane >> 5;
+    const int operand = ((in_row >> 4) * BLOCK) + ((in_row & 15) + 16 * half) * 16;
+
+#pragma unroll
+    for (int s = 0; s < STAGES - 1; s++) issue(s);
+    for (int step = 0; step < steps; step++) {
+        stage_barrier<PER_WAVE * (STAGES - 2)>();
+        issue(step + STAGES - 1);   // into the stage read one step ago; past the end it loads the last step again
+        const LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
+#pragma unroll
+        for (int sub = 0; sub < 2; sub++) {
+            typename MMA::Operand af[FM];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                af[i] = *(const LDS_SPACE typename MMA::Operand*)(stage + ((wm * WM + i * 32) / 16) * BLOCK + operand + sub * 32 * 16);
+#pragma unroll
+            for (int g = 0; g < NB; g++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    const typename MMA::Operand bf =
+                        *(const LDS_SPACE typename MMA::Operand*)(stage + (A_BLOCKS + (g * BN + wn * WN + j * 32) / 16) * BLOCK + operand + sub * 32 * 16);
+#pragma unroll
+                    for (int i = 0; i < FM; i++) acc[g][i][j] = MMA::step(bf, af[i], acc[g][i][j]);
+                }
+        }
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
+    bare_barrier();
+
+    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the f32 tile in LDS ([BM][BN + 4]).
+    // A fragment's lane holds row lane % 32 and, in register 4 q + r, column 8 q + 4 (lane / 32) + r.
+    float* staged = (float*)lds;
+    const bool quads = N % 4 == 0;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        const int m_local = wm * WM + i * 32 + in_row;
+        const float xs = (INT8 && !RAW) ? e.x_scale[min(m0 + m_local, M - 1)] : 1.0f;
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int n_local = wn * WN + j * 32 + 8 * q + 4 * half;
+                const int n = n0 + n_local;
+                float value[4];
+                if constexpr (RAW) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) value[r] = __int_as_float((int)acc[0][i][j][4 * q + r]);
+                } else {
+                    float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f}, ws_up[4] = {1.0f, 1.0f, 1.0f, 1.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+                    if (quads && n < N) {
+                        if constexpr (INT8) {
+                            const float4 s4 = *reinterpret_cast<const float4*>(e.w_scale + n);
+                            ws[0] = s4.x; ws[1] = s4.y; ws[2] = s4.z; ws[3] = s4.w;
+                            if constexpr (NB == 2) {
+                                const float4 u4 = *reinterpret_cast<const float4*>(e.w_scale + N + n);
+                                ws_up[0] = u4.x; ws_up[1] = u4.y; ws_up[2] = u4.z; ws_up[3] = u4.w;
+                            }
+                        }
+                        if (e.flags & EPI_BIAS) {
+                            const v4h b4 = quad_halves(e.bias + n);
+#pragma unroll
+                            for (int r = 0; r < 4; r++) b[r] = (float)b4[r];
+                        }
+                    } else {
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            if (n + r < N) {
+                                if constexpr (INT8) {
+                                    ws[r] = e.w_scale[n + r];
+                                    if constexpr (NB == 2) ws_up[r] = e.w_scale[N + n + r];
+                                }
+                                if (e.flags & EPI_BIAS) b[r] = (float)e.bias[n + r];
+                            }
+                    }
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        if constexpr (INT8) {
+                            value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws[r];
+                        } else {
+                            value[r] = MMA::value(acc[0][i][j], 4 * q + r);
+                        }
+                        if (e.flags & EPI_BIAS) value[r] = value[r] + b[r];
+                        if constexpr (NB == 2) {
+                            const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up[r] : MMA::value(acc[1][i][j], 4 * q + r);
+                            value[r] = silu_fast(value[r]) * up;
+                        }
+                    }
+                }
+                *reinterpret_cast<float4*>(staged + m_local * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
+            }
+    }
+    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
+    bare_barrier();
+
+    // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
+    // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
+    constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES;
+    const bool vectors = N % 8 == 0;
+    float rs = 0.0f, is = 0.0f;
+    if (e.flags & EPI_MIX) {
+        rs = (float)e.residual_scale[0];
+        is = (float)e.input_scale[0];
+    }
+#pragma unroll
+    for (int pass = 0; pass < BM / ROWS; pass++) {
+        const int m_local = pass * ROWS + tid / ROW_LANES, n_local = (tid % ROW_LANES) * 8;
+        const int m = m0 + m_local, n = n0 + n_local;
+        if (m >= M || n >= N) continue;
+        const size_t at = (size_t)m * N + n;
+        const float4 lo = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local);
+        const float4 hi = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local + 4);
+        float value[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+        if constexpr (RAW) {
+            if (vectors) {
+                *reinterpret_cast<uint4*>(out + at) = uint4{__float_as_uint(value[0]), __float_as_uint(value[1]), __float_as_uint(value[2]), __float_as_uint(value[3])};
+                *reinterpret_cast<uint4*>(out + at + 4) = uint4{__float_as_uint(value[4]), __float_as_uint(value[5]), __float_as_uint(value[6]), __float_as_uint(value[7])};
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+                    if (n + c < N) out[at + c] = __float_as_int(value[c]);
+            }
+        } else {
+            if (e.flags & EPI_RESIDUAL) {
+                if (vectors) {
+                    const v8h res = *reinterpret_cast<const v8h*>(e.residual + at);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) value[c] = value[c] + (float)res[c];
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) value[c] = value[c] + (float)e.residual[at + c];
+                }
+            }
+            if (e.flags & EPI_MIX) {
+                float original[8];
+                if (vectors) {
+                    const v8h o = *reinterpret_cast<const v8h*>(e.original + at);
+#pragma unroll
+                    for (int c = 0; c < 8; c++) original[c] = (float)o[c];
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
+                }
+#pragma unroll
+                for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
+            }
+            if (vectors) {
+                store_eight<OutT>(out + at, value);
+            } else {
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+                    if (n + c < N) out[at + c] = from_float<OutT>(value[c]);
+            }
+        }
+    }
+}
+
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT>
+int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
+    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = BM * (BN + 4) * 4;
+    constexpr int BYTES = RING > STAGING ? RING : STAGING;
+    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT>;
+    if (BYTES > 65536) {
+        static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
+        if (allowed != hipSuccess) return (int)allowed;
+    }
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(THREADS), BYTES, stream, (const In*)x, (const In*)w, (OutT*)out, e, M, N, K);
+    return launch_status();
+}
+
+constexpr int TILES = 6;
+
+// The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
+// 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
+// 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4). 0 picks by the launch's size.
+template <typename In, int NB, typename OutT>
+int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    if (tile == 0) {
+        const long large = (long)((M + 255) / 256) * ((N + 127) / 128);
+        tile = large >= 512 ? 4 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
+    }
+    switch (tile) {
+        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
+        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
+        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
+        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT>(x, w, out, e, M, N, K, stream);
+        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT>(x, w, out, e, M, N, K, stream);
+        default: return launch<In, 256, 64, 4, 1, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
+    }
+}
+
+int check(const void* x, const void* w, void* out, int M, int N, int K, int depth, int tile, const char* what) {
+    if (M < 0 || N <= 0 || K <= 0) return chess_fail(CHESS_INVALID_SHAPE, "%s: M %d, N %d, K %d", what, M, N, K);
+    if (K % depth != 0) return chess_fail(CHESS_INVALID_SHAPE, "%s reads the %d inputs %d at a time", what, K, depth);
+    if (!x || !w || !out) return chess_fail(CHESS_INVALID_SHAPE, "%s: a required pointer is null", what);
+    if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return chess_fail(CHESS_MISALIGNED, "%s's 16-byte loads need aligned x, w and out", what);
+    if (tile < 0 || tile > TILES) return chess_fail(CHESS_UNSUPPORTED, "tile %d is none of 0 (by size) to %d", tile, TILES);
+    return CHESS_OK;
+}
+
+int check_epilogue(const void* bias, const void* residual, const void* original, const void* residual_scale, const void* input_scale,
+                   const char* what) {
+    if (original && (!residual_scale || !input_scale))
+        return chess_fail(CHESS_INVALID_SHAPE, "%s's input mix needs the residual and input scales", what);
+    if ((bias && ((uintptr_t)bias & 7u)) || (residual && !aligned16(residual)) || (original && !aligned16(original)))
+        return chess_fail(CHESS_MISALIGNED, "%s's epilogue reads bias and residual 4 and 8 columns at a time", what);
+    return CHESS_OK;
+}
+
+}  // namespace
+
+extern "C" int chess_int8_linear(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* bias,
+                                 const void* residual, const void* original, const void* residual_scale, const void* input_scale,
+                                 void* out, int M, int N, int K, int gated, int out_dtype, int tile, void* stream)
+{
+    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES, tile, "int8_linear")) return status;
+    if (int status = check_epilogue(bias, residual, original, residual_scale, input_scale, "int8_linear")) return status;
+    if (!x_scale || !w_scale) return chess_fail(CHESS_INVALID_SHAPE, "int8_linear needs both scales");
+    if (!aligned16(w_scale)) return chess_fail(CHESS_MISALIGNED, "int8_linear reads the weight scales 4 at a time");
+    if (out_dtype != OUT_F16 && out_dtype != OUT_BF16) return chess_fail(CHESS_UNSUPPORTED, "int8_linear writes fp16 or bf16, not %d", out_dtype);
+    if (M == 0) return CHESS_OK;
+    Epilogue e{(const float*)x_scale, (const float*)w_scale, (const half_t*)bias, (const half_t*)residual, (const half_t*)original,
+               (const half_t*)residual_scale, (const half_t*)input_scale,
+               (bias ? EPI_BIAS : 0) | (residual ? EPI_RESIDUAL : 0) | (original ? EPI_MIX : 0)};
+    hipStream_t s = (hipStream_t)stream;
+    if (gated) {
+        return out_dtype == OUT_F16 ? dispatch<int8_t, 2, half_t>(x, w, out, e, M, N, K, tile, s)
+                                    : dispatch<int8_t, 2, bf16_t>(x, w, out, e, M, N, K, tile, s);
+    }
+    return out_dtype == OUT_F16 ? dispatch<int8_t, 1, half_t>(x, w, out, e, M, N, K, tile, s)
+                                : dispatch<int8_t, 1, bf16_t>(x, w, out, e, M, N, K, tile, s);
+}
+
+extern "C" int chess_int8_matmul_i32(const void* x, const void* w, void* out, int M, int N, int K, int tile, void* stream)
+{
+    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES, tile, "int8_matmul_i32")) return status;
+    if (M == 0) return CHESS_OK;
+    Epilogue e{nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0};
+    return dispatch<int8_t, 1, int>(x, w, out, e, M, N, K, tile, (hipStream_t)stream);
+}
+
+extern "C" int chess_linear(const void* x, const void* w, const void* bias, const void* residual, const void* original,
+                            const void* residual_scale, const void* input_scale, void* out, int M, int N, int K, int gated, int out_dtype, int tile,
+                            void* stream)
+{
+    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES / 2, tile, "linear")) return status;
+    if (int status = check_epilogue(bias, residual, original, residual_scale, input_scale, "linear")) return status;
+    if (out_dtype != OUT_F16 && out_dtype != OUT_F32) return chess_fail(CHESS_UNSUPPORTED, "linear writes fp16 or f32, not %d", out_dtype);
+    if (M == 0) return CHESS_OK;
+    Epilogue e{nullptr, nullptr, (const half_t*)bias, (const half_t*)residual, (const half_t*)original, (const half_t*)residual_scale,
+               (const half_t*)input_scale, (bias ? EPI_BIAS : 0) | (residual ? EPI_RESIDUAL : 0) | (original ? EPI_MIX : 0)};
+    hipStream_t s = (hipStream_t)stream;
+    if (gated) {
+        return out_dtype == OUT_F16 ? dispatch<half_t, 2, half_t>(x, w, out, e, M, N, K, tile, s)
+                                    : dispatch<half_t, 2, float>(x, w, out, e, M, N, K, tile, s);
+    }
+    return out_dtype == OUT_F16 ? dispatch<half_t, 1, half_t>(x, w, out, e, M, N, K, tile, s) : dispatch<half_t, 1, float>(x, w, out, e, M, N, K, tile, s);
+}

@@ -9,6 +9,7 @@ torch operations on the GPU, which is the reference's own path on GPUs without i
 from __future__ import annotations
 
 import math
+import threading
 
 import torch
 import torch.nn.functional as F
@@ -20,8 +21,8 @@ from model.hip_kernels import aligned, check, library_for, pointer, stream_of
 from model.model import ChessTransformer, TransformerBlock
 
 LINEAR_DEPTH, GROUP_M = 32, 8
-# linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185): 1 has 64-row tiles, 2 128-row
-LINEAR_TILES = {"gfx950": [(64, 1), (math.inf, 2)]}
+# linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
+LINEAR_TILES = {"gfx950": [(16, 1), (64, 3), (math.inf, 2)]}
 # positions a launch should reach before a workgroup takes several key/value groups
 ATTENTION_WORKGROUPS = 1024
 
@@ -82,6 +83,30 @@ def _(projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_c
     return projected.new_empty(B, T, heads * dv)
 
 
+# by data_ptr: (the K x N weight, its version, its N x K copy); the entry holds the weight so that its memory is not another's
+TRANSPOSED: dict[int, tuple[torch.Tensor, int, torch.Tensor]] = {}
+TRANSPOSED_MOST = 512
+TRANSPOSED_LOCK = threading.Lock()
+
+
+def transposed_weight(weight: torch.Tensor) -> torch.Tensor:
+    """The N x K copy of a K x N weight that the kernel reads (both its operands are read along K), made once per weight and
+    version outside graph recording, as the reference pairs its templates once (attention_cuda.py:410-440)."""
+    version = 0 if weight.is_inference() else weight._version
+    found = TRANSPOSED.get(weight.data_ptr())
+    if found is not None and found[1] == version and found[0].shape == weight.shape:
+        return found[2]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("linear's weight was not seen before the graph recording began (run the model once first)")
+    with torch.no_grad():
+        copy = weight.detach().t().contiguous()
+    with TRANSPOSED_LOCK:
+        TRANSPOSED[weight.data_ptr()] = (weight, version, copy)
+        while len(TRANSPOSED) > TRANSPOSED_MOST:
+            del TRANSPOSED[next(iter(TRANSPOSED))]
+    return copy
+
+
 def launch_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, residual: torch.Tensor | None, gated: bool,
                   accumulate_fp32: bool, original: torch.Tensor | None, residual_scale: torch.Tensor | None, input_scale: torch.Tensor | None,
                   tile: int = 0) -> torch.Tensor:
@@ -96,7 +121,8 @@ def launch_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
         if tensor is not None and tensor.dtype != torch.float16:
             raise ValueError(f"linear's {name} is {tensor.dtype}, the kernel takes fp16")
     library = library_for(x.device)
-    x, weight, residual, original = aligned(x), aligned(weight), aligned(residual), aligned(original)
+    x, residual, original = aligned(x), aligned(residual), aligned(original)
+    weight = aligned(transposed_weight(weight))
     M = x.numel() // K
     out = x.new_empty(*x.shape[:-1], N, dtype=torch.float32 if accumulate_fp32 else torch.float16)
     code = library.chess_linear(pointer(x), pointer(weight), pointer(bias.contiguous() if bias is not None else None), pointer(residual),

@@ -23,12 +23,11 @@ from model.hip_kernels import aligned, check, library_for, pointer, stream_of
 HADAMARD_BLOCK = 32
 DOWN_INPUT_MULTIPLE = 128
 INT8_DEPTH = 64
-# The GEMM's tiles by the rows a compute unit's share is (the reference's table format, int8_blocks.py:19-31):
-# tile 1 has 64-row tiles, 2 has 128-row tiles. Every tile gives the same bits.
-SMALL_TILE, LARGE_TILE = 1, 2
-INT8_TILES = {"gfx950": {"projection": [(64, SMALL_TILE), (math.inf, LARGE_TILE)],
-                         "gate_up": [(64, SMALL_TILE), (math.inf, LARGE_TILE)],
-                         "down": [(128, SMALL_TILE), (math.inf, LARGE_TILE)]}}
+# The GEMM's tiles by the rows a compute unit's share is (the reference's table format, int8_blocks.py:19-31), timed on an
+# MI355X: 1 is 64 x 64, 2 128 x 128, 3 128 x 64, 4 256 x 128 (rows x outputs). Every tile gives the same bits.
+INT8_TILES = {"gfx950": {"projection": [(16, 1), (64, 3), (math.inf, 4)],
+                         "gate_up": [(16, 1), (64, 3), (math.inf, 4)],
+                         "down": [(16, 1), (64, 3), (math.inf, 2)]}}
 # rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit
 NORM_ROWS = 4
 ROTATE_ROWS = 4

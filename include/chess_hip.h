@@ -59,10 +59,11 @@ int chess_template_attention(const void* projected, const void* templates, const
                              int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block, float eps,
                              float scale, void* stream);
 
-/* out[M, N] = epilogue(x[M, K] @ w[K, N(x2 if gated)]), x and w fp16 (w in_features x out_features),
- * f32 sums; epilogue + bias, silu(gate) * up, + residual, input mix as chess_int8_linear; fp16 or f32
- * (accumulate_fp32) out. K % 32 == 0, N % 8 == 0. Replaces linear_kernel / launch_linear
- * (model/fused_blocks.py:229-304) behind the op linear (:308-318). */
+/* out[M, N] = epilogue(x[M, K] @ W[K, N(x2 if gated)]), x and W fp16 (W in_features x out_features), f32 sums,
+ * taken as w = W^T, row-major [N(x2), K] (the gate's rows, then up's); epilogue + bias, silu(gate) * up,
+ * + residual, input mix as chess_int8_linear; fp16 or f32 (accumulate_fp32) out. K % 32 == 0; tile as
+ * chess_int8_linear. Replaces linear_kernel / launch_linear (model/fused_blocks.py:229-304) behind the op
+ * linear (:308-318), whose K x N weight the Python layer transposes once. */
 int chess_linear(const void* x, const void* w, const void* bias, const void* residual, const void* original, const void* residual_scale,
                  const void* input_scale, void* out, int M, int N, int K, int gated, int out_dtype, int tile, void* stream);
 

@@ -60,7 +60,7 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 7, 0, None) == hip_kernels.UNSUPPORTED
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, 16, None, None, 16, 4, 8, 64, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_matmul_i32(MISALIGNED, 16, 16, 4, 8, 64, 0, None) == hip_kernels.MISALIGNED
-    assert library.chess_int8_matmul_i32(16, 16, 16, 4, 8, 64, 3, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_int8_matmul_i32(16, 16, 16, 4, 8, 64, 7, None) == hip_kernels.UNSUPPORTED
     attention = lambda *shape: library.chess_template_attention(16, 16, 16, 16, 16, *shape, 1e-5, 0.125, None)
     assert attention(1, 32, 8, 8, 64, 64, 8, 1) == hip_kernels.UNSUPPORTED            # fewer than 64 tokens
     assert attention(1, 70, 8, 3, 64, 64, 8, 1) == hip_kernels.INVALID_SHAPE           # 3 key/value heads for 8
@@ -69,7 +69,6 @@ def test_refused_shapes_come_back_as_codes(library):
     assert attention(1, 70, 8, 8, 64, 64, 9, 1) == hip_kernels.UNSUPPORTED             # 9 templates
     assert attention(1, 70, 8, 8, 64, 64, 8, 3) == hip_kernels.INVALID_SHAPE           # 3 groups a workgroup for 8
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
-    assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 12, 64, 0, 0, 0, None) == hip_kernels.UNSUPPORTED
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
 
 
