@@ -7,6 +7,8 @@ attention configs, the roofline of the dominant kernel (timed with HIP events on
 baseline (the CPU oracle's fp32 forward, the reference's CPU path, on a bounded sample, on this host's cores).
 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024] [--sweep] [--no-cpu]
+python bench.py --kernel-only      the dominant kernel and a plain copy alone, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
+python bench.py --pmc-summary DIR  reads those two runs' counter_collection.csv files and prints the HBM bytes per launch
 """
 from __future__ import annotations
 
@@ -28,6 +30,13 @@ FP16_PEAK_TFLOPS = 2500.0    # dense fp16/bf16 MFMA
 HBM_PEAK_GBS = 8000.0
 SETTINGS = {"d_model": 512, "num_layers": 28, "n_heads": 8, "kv_heads": 8, "mlp_hidden": 2048, "value_bins": 128, "position_templates": 8}
 TOKENS = 70
+# the GEMM's tiles (rows x outputs, waves, ring stages), as chess_int8_linear numbers them
+GEMM_TILES = {1: "64x64, 4 waves, 4 stages", 2: "128x128, 4 waves, 4 stages", 3: "128x64, 4 waves, 4 stages", 4: "256x128, 4 waves, 3 stages",
+              5: "128x256, 4 waves, 3 stages", 6: "256x64, 4 waves, 4 stages"}
+# HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a plain copy's counters
+TRAFFIC = ROOT / "profiles" / "gate_up_gemm_batch1024_traffic.json"
+COPY_BYTES = 1 << 29
+MI355X_CUS = 256
 
 
 def log(message: str) -> None:
@@ -175,6 +184,85 @@ def standalone_attention(device) -> dict:
             "bytes": moved, "positions": B}
 
 
+def gate_up_case(device, batch: int, weight=None, weight_scale=None):
+    """The dominant kernel at the network's shape: the gated gate_up GEMM of an int8 block (2 x 2048 weight rows, depth 512) over the
+    batch's rows, with the tile the network picks; returns (launch, rows, tile)."""
+    import torch
+    from engine.quantization import nearest
+    from model.int8_blocks import int8_tile, launch_int8_linear
+    M = batch * TOKENS
+    generator = torch.Generator(device=device).manual_seed(5)
+    x = torch.randint(-127, 128, (M, 512), device=device, dtype=torch.int8, generator=generator)
+    x_scale = torch.rand(M, device=device, generator=generator) / 100
+    if weight is None:
+        weight, weight_scale = nearest(torch.randn(2 * 2048, 512, device=device, generator=generator) * 0.02)
+        weight, weight_scale = weight.to(device), weight_scale.to(device)
+    tile = int8_tile(device, "gate_up", M)
+    return (lambda: launch_int8_linear(x, x_scale, weight, weight_scale, None, None, True, None, None, None, tile)), M, tile
+
+
+def dominant_kernel(device, network, batch: int) -> dict:
+    block = network.encoder[0]
+    launch, M, tile = gate_up_case(device, batch, block.gate_up, block.gate_up_scale)
+    ms = time_kernel(launch)
+    ops = 2 * M * (2 * 2048) * 512
+    achieved = ops / ms / 1e9
+    traffic = json.loads(TRAFFIC.read_text()) if TRAFFIC.exists() else None
+    if traffic is not None and (traffic.get("rows") != M or traffic.get("tile") != tile):
+        traffic = None
+    return {"kernel": f"gemm_kernel<int8> tile {tile} ({GEMM_TILES[tile]}), gate_up with the gated SiLU epilogue", "bound": "mfma",
+            "achieved": round(achieved, 1), "peak": INT8_PEAK_TOPS, "unit": "TOPS", "frac": round(achieved / INT8_PEAK_TOPS, 4),
+            "traffic": traffic["hbm_bytes"] if traffic else None, "ops_per_launch": ops, "avg_launch_ms": round(ms, 4), "rows": M,
+            "algorithmic_bytes": M * 512 + 4096 * 512 + 4 * M + 4 * 4096 + 2 * M * 2048}
+
+
+def kernel_only(batch: int, repeats: int = 20) -> int:
+    """The dominant kernel and a copy of COPY_BYTES alone, for counter runs: the copy's FETCH_SIZE / WRITE_SIZE give the
+    counters' scale."""
+    import torch
+    device = torch.device("cuda", 0)
+    launch, M, tile = gate_up_case(device, batch)
+    source = torch.empty(COPY_BYTES, device=device, dtype=torch.uint8).random_(0, 255)
+    target = torch.empty_like(source)
+    for _ in range(repeats):
+        launch()
+        target.copy_(source)
+    torch.cuda.synchronize()
+    log(f"kernel-only: {repeats} launches of gate_up tile {tile} over {M} rows and {repeats} copies of {COPY_BYTES} bytes")
+    return 0
+
+
+def pmc_summary(folder: Path, batch: int) -> int:
+    """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, KiB per dispatch), each
+    scaled by what the counter reads for the copy of COPY_BYTES."""
+    import csv
+    from model.fused_blocks import tile_for
+    from model.int8_blocks import INT8_TILES
+    values: dict[str, dict[str, list[float]]] = {}
+    for path in sorted(folder.rglob("*counter_collection.csv")):
+        for row in csv.DictReader(path.open()):
+            values.setdefault(row["Counter_Name"], {}).setdefault(row["Kernel_Name"], []).append(float(row["Counter_Value"]))
+    mean = {}
+    for counter, kernels in values.items():
+        averages = {name: sum(v) / len(v) for name, v in kernels.items()}
+        # the copy of COPY_BYTES is the largest copy the run makes; the GEMM is the only gemm_kernel
+        copies = [name for name in averages if "copy" in name.lower()]
+        gemms = [name for name in averages if "gemm_kernel" in name]
+        mean[counter] = {"copy": max(averages[name] for name in copies), "gemm": averages[gemms[0]]}
+    fetch_scale = COPY_BYTES / (mean["FETCH_SIZE"]["copy"] * 1024)
+    write_scale = COPY_BYTES / (mean["WRITE_SIZE"]["copy"] * 1024)
+    fetch = mean["FETCH_SIZE"]["gemm"] * 1024 * fetch_scale
+    write = mean["WRITE_SIZE"]["gemm"] * 1024 * write_scale
+    M = batch * TOKENS
+    result = {"rows": M, "tile": tile_for(INT8_TILES["gfx950"]["gate_up"], M, MI355X_CUS), "hbm_bytes": round(fetch + write), "fetch_bytes": round(fetch), "write_bytes": round(write),
+              "fetch_kib_raw": mean["FETCH_SIZE"]["gemm"], "write_kib_raw": mean["WRITE_SIZE"]["gemm"],
+              "copy_fetch_kib": mean["FETCH_SIZE"]["copy"], "copy_write_kib": mean["WRITE_SIZE"]["copy"],
+              "fetch_scale": round(fetch_scale, 4), "write_scale": round(write_scale, 4),
+              "algorithmic_bytes": M * 512 + 4096 * 512 + 4 * M + 4 * 4096 + 2 * M * 2048}
+    print(json.dumps(result))
+    return 0
+
+
 def cpu_baseline(model_state: dict, sample: int) -> dict:
     """The CPU oracle's fp32 forward (the reference's CPU path, model/model.py:245-270) on a bounded sample, this host's cores."""
     import torch
@@ -201,16 +289,21 @@ def main() -> int:
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     parser.add_argument("--cpu-sample", type=int, default=256)
     parser.add_argument("--no-standalone", action="store_true", help="skip the standalone GEMM and attention configs")
+    parser.add_argument("--kernel-only", action="store_true", help="run only the dominant kernel and a copy, for counter runs")
+    parser.add_argument("--pmc-summary", type=Path, help="summarise the FETCH_SIZE / WRITE_SIZE runs under this folder")
     arguments = parser.parse_args()
+    if arguments.pmc_summary:
+        return pmc_summary(arguments.pmc_summary, arguments.batch)
     if arguments.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one and nothing in this build uses a second (asked for {arguments.gpus})",
               file=sys.stderr)
         return 2
+    if arguments.kernel_only:
+        return kernel_only(arguments.batch)
 
     import torch
     from engine.inference import int8_network
     from engine.quantization import nearest_int8_weights
-    from model.int8_blocks import launch_int8_linear
 
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)
@@ -227,15 +320,17 @@ def main() -> int:
     log(f"  {ms_per_step:.3f} ms/step, {positions_per_s:,.0f} positions/s")
     del graphed
 
-    log(f"batch {arguments.latency_batch}: latency over 200 replays")
-    small = Graphed(network, arguments.latency_batch, device)
-    _, latencies = time_graph(small, 200, 20)
-    latencies.sort()
-    p50, p99 = latencies[len(latencies) // 2], latencies[int(len(latencies) * 0.99) - 1]
-    latency = {"batch": arguments.latency_batch, "p50_ms": round(p50, 4), "p99_ms": round(p99, 4),
-               "positions_per_s": round(arguments.latency_batch / (p50 / 1e3), 1)}
-    log(f"  p50 {p50:.3f} ms, p99 {p99:.3f} ms")
-    del small
+    latency = None
+    if arguments.latency_batch > 0:
+        log(f"batch {arguments.latency_batch}: latency over 200 replays")
+        small = Graphed(network, arguments.latency_batch, device)
+        _, latencies = time_graph(small, 200, 20)
+        latencies.sort()
+        p50, p99 = latencies[len(latencies) // 2], latencies[int(len(latencies) * 0.99) - 1]
+        latency = {"batch": arguments.latency_batch, "p50_ms": round(p50, 4), "p99_ms": round(p99, 4),
+                   "positions_per_s": round(arguments.latency_batch / (p50 / 1e3), 1)}
+        log(f"  p50 {p50:.3f} ms, p99 {p99:.3f} ms")
+        del small
 
     sweep = {}
     if arguments.sweep:
@@ -247,20 +342,8 @@ def main() -> int:
             log(f"  sweep batch {batch}: {ms:.3f} ms, {batch / ms * 1e3:,.0f} positions/s")
             del graphed
 
-    # the dominant kernel: the gated gate_up GEMM of an int8 block at the batch's rows (2 x 2048 weight rows, depth 512)
-    M = arguments.batch * TOKENS
-    block = network.encoder[0]
-    generator = torch.Generator(device=device).manual_seed(5)
-    x = torch.randint(-127, 128, (M, 512), device=device, dtype=torch.int8, generator=generator)
-    x_scale = torch.rand(M, device=device, generator=generator) / 100
-    gate_up_ms = time_kernel(lambda: launch_int8_linear(x, x_scale, block.gate_up, block.gate_up_scale, None, None, True, None, None, None))
-    gate_up_ops = 2 * M * (2 * 2048) * 512
-    achieved = gate_up_ops / gate_up_ms / 1e9
-    roofline = {"kernel": "int8_gemm_kernel<128,64,2,fp16> (gate_up, silu epilogue)", "bound": "mfma", "achieved": round(achieved, 1),
-                "peak": INT8_PEAK_TOPS, "unit": "TOPS", "frac": round(achieved / INT8_PEAK_TOPS, 4), "traffic": None,
-                "ops_per_launch": gate_up_ops, "avg_launch_ms": round(gate_up_ms, 4), "rows": M}
-    log(f"gate_up GEMM: {gate_up_ms:.3f} ms, {achieved:.0f} TOPS ({achieved / INT8_PEAK_TOPS:.1%} of dense int8 peak)")
-    del x, x_scale
+    roofline = dominant_kernel(device, network, arguments.batch)
+    log(f"gate_up GEMM: {roofline['avg_launch_ms']:.3f} ms, {roofline['achieved']:.0f} TOPS ({roofline['frac']:.1%} of dense int8 peak)")
 
     standalone = {}
     if not arguments.no_standalone:
