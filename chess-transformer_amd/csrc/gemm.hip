@@ -21,9 +21,10 @@
 // K advances a stage at a time through a ring of STAGES stages in LDS, filled by the DMA loads
 // global_load_lds_dwordx4 (global memory straight to LDS, no registers): STAGES - 1 stages are in flight
 // while one is multiplied, and a wavefront waits (s_waitcnt vmcnt) only for the stage it is about to read.
-// A stage holds 1 KB blocks of 16 rows x 64 bytes, a DMA instruction's 64 lanes each writing 16 bytes; a
-// row's 16-byte chunk c sits at lane (row + 16 c), so the 16 lanes of an MFMA operand group read 256
-// contiguous bytes (no bank conflicts) and a DMA instruction reads 64 contiguous bytes of each of 16 rows.
+// A stage holds 1 KB blocks of 16 rows x 64 bytes, a DMA instruction's 64 lanes each writing 16 bytes at
+// 16 x lane. Lanes 4 r .. 4 r + 3 read row r's 64 bytes, so neighbouring lanes read neighbouring bytes (the
+// load path is 3x slower when they are a row apart); lane 4 r + j takes chunk j ^ (r / 4), an XOR swizzle
+// under which the 16 rows an MFMA operand group reads sit in 16 different 16-byte LDS bank groups.
 // An MFMA operand lane holds 16 consecutive bytes of one row (16 int8 or 8 fp16); which k a byte stands
 // for is the same for both operands, so the sums are the dot products whatever the hardware's k order. The
 // weights are the MFMA's first operand: a lane's results are then groups of 4 consecutive columns of one
@@ -135,14 +136,14 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const int m0 = (first_m + tile % in_group % group_rows) * BM;
     const int n0 = (tile % in_group / group_rows) * BN;
 
-    // this lane's source in each of the wavefront's blocks: row (lane % 16) of the block, 16-byte chunk lane / 16.
+    // this lane's source in each of the wavefront's blocks: row lane / 4 of the block, 16-byte chunk (lane % 4) ^ (lane / 16).
     // Rows past M read row M - 1 and columns past N read column N - 1: their sums are never stored.
     const int8_t* source[PER_WAVE];
 #pragma unroll
     for (int p = 0; p < PER_WAVE; p++) {
         const int block = wave * PER_WAVE + p;
-        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * 16 + (lane & 15);
-        const int chunk = (lane >> 4) * 16;
+        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * 16 + (lane >> 2);
+        const int chunk = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
         if (block < A_BLOCKS) {
             source[p] = (const int8_t*)x + (size_t)min(m0 + row, M - 1) * row_bytes + chunk;
         } else {
@@ -169,9 +170,12 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
                 for (int r = 0; r < 16; r++) acc[g][i][j][r] = 0;
 
-    // an operand lane (row lane % 32, 16-byte half lane / 32) in a stage: the block of its 16 rows, then row + 16 chunk
-    const int in_row = lane & 31, half = lane >> 5;
-    const int operand = ((in_row >> 4) * BLOCK) + ((in_row & 15) + 16 * half) * 16;
+    // an operand lane (row lane % 32, 16-byte half lane / 32 of each 32-byte sub-step) in a stage: the block of its
+    // 16 rows, then the slot 4 r + (chunk ^ (r / 4)) of row r's chunk
+    const int in_row = lane & 31, half = lane >> 5, r16 = in_row & 15;
+    int operand[2];
+#pragma unroll
+    for (int sub = 0; sub < 2; sub++) operand[sub] = (in_row >> 4) * BLOCK + (r16 * 4 + ((half + 2 * sub) ^ (r16 >> 2))) * 16;
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++) issue(s);
@@ -184,13 +188,13 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
             typename MMA::Operand af[FM];
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                af[i] = *(const LDS_SPACE typename MMA::Operand*)(stage + ((wm * WM + i * 32) / 16) * BLOCK + operand + sub * 32 * 16);
+                af[i] = *(const LDS_SPACE typename MMA::Operand*)(stage + ((wm * WM + i * 32) / 16) * BLOCK + operand[sub]);
 #pragma unroll
             for (int g = 0; g < NB; g++)
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     const typename MMA::Operand bf =
-                        *(const LDS_SPACE typename MMA::Operand*)(stage + (A_BLOCKS + (g * BN + wn * WN + j * 32) / 16) * BLOCK + operand + sub * 32 * 16);
+                        *(const LDS_SPACE typename MMA::Operand*)(stage + (A_BLOCKS + (g * BN + wn * WN + j * 32) / 16) * BLOCK + operand[sub]);
 #pragma unroll
                     for (int i = 0; i < FM; i++) acc[g][i][j] = MMA::step(bf, af[i], acc[g][i][j]);
                 }

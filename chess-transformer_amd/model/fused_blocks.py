@@ -22,7 +22,7 @@ from model.model import ChessTransformer, TransformerBlock
 
 LINEAR_DEPTH, GROUP_M = 32, 8
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
-LINEAR_TILES = {"gfx950": [(16, 1), (64, 3), (math.inf, 2)]}
+LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 3)]}
 # positions a launch should reach before a workgroup takes several key/value groups
 ATTENTION_WORKGROUPS = 1024
 
