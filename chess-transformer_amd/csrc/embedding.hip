@@ -1,0 +1,156 @@
+// The network's input: boards of T token codes in, out[B, T, D] fp16 =
+//   f16( (f32(embed[code]) + f32(position[t])) + f32(f16(sum over the 23 square features of table[row])) )
+// the last term for the 64 square tokens only, its rows found from the board itself, as
+// model/fused_blocks.py:412-469 (board_embedding_kernel) and model/model.py:128-174 (SquareFeatures.indices)
+// find them: where the kings and queens are from the square, the codes of its 8 neighbours, the first piece
+// along each of 8 lines and how far out, the knights attacking it, the nearest pawn up and down its file.
+// The features are summed in f32 in their slot order (0..22), then rounded to fp16 (model/fused_blocks.py:383-393).
+//
+// A workgroup takes one board: its 64 squares' 23 rows are found by one thread a square into LDS, then
+// every (token, 8 columns) item gathers its rows 16 bytes a lane. Row numbers are clamped into the table
+// (and codes into the embedding), so that a board with codes the encoding never makes reads no memory
+// outside the tables.
+#include "chess_common.h"
+
+namespace {
+
+constexpr int SQUARES = 64;
+constexpr int FEATURES = 23;
+constexpr int STEPS = 8;          // a ray's squares, nearest first: 7 and a pad, 64 past the edge
+
+struct Codes {
+    int pawn, knight, queen, king, theirs, edge, no_piece;
+};
+
+template <typename Code>
+__global__ __launch_bounds__(256) void board_embedding_kernel(
+    const Code* __restrict__ boards, const int* __restrict__ rays, const int* __restrict__ jumps, const int* __restrict__ offsets,
+    const half_t* __restrict__ embed, const half_t* __restrict__ position, const half_t* __restrict__ table, half_t* __restrict__ out,
+    int T, int D, int embed_rows, int table_rows, Codes codes)
+{
+    __shared__ int square_codes[SQUARES + 1];     // the 65th is the code past the edge
+    __shared__ int token_codes[128];
+    __shared__ int first[4];
+    __shared__ int rows[SQUARES][FEATURES + 1];
+
+    const int tid = threadIdx.x;
+    const size_t b = blockIdx.x;
+    const Code* board = boards + b * T;
+    if (tid < T) {
+        const int code = (int)board[tid];
+        token_codes[tid] = min(max(code, 0), embed_rows - 1);
+        if (tid < SQUARES) square_codes[tid] = code;
+    }
+    if (tid == SQUARES) square_codes[SQUARES] = codes.edge;
+    if (tid < 4) first[tid] = SQUARES;
+    __syncthreads();
+    const int pieces[4] = {codes.king, codes.king + codes.theirs, codes.queen, codes.queen + codes.theirs};
+    if (tid < SQUARES) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            if (square_codes[tid] == pieces[i]) atomicMin(&first[i], tid);
+    }
+    __syncthreads();
+
+    if (tid < SQUARES) {
+        const int s = tid, file = s % 8, rank = s / 8;
+        int row[FEATURES];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int p = first[i];
+            row[i] = p < SQUARES ? (rank - p / 8 + 7) * 15 + file - p % 8 + 7 : codes.no_piece;
+        }
+        const int pawn_theirs = codes.pawn + codes.theirs;
+#pragma unroll
+        for (int d = 0; d < 8; d++) {
+            const int* ray = rays + (s * 8 + d) * STEPS;
+            int line = 0, pawn = 0;
+            bool line_found = false, pawn_found = false;
+#pragma unroll
+            for (int k = 0; k < STEPS; k++) {
+                const int at = min(max(ray[k], 0), SQUARES);
+                const int code = square_codes[at];
+                if (k == 0) row[4 + d] = code;
+                if (!line_found && code != 0 && code != codes.edge) {
+                    line = 1 + (code - 1) * 7 + k;
+                    line_found = true;
+                }
+                if (d < 2 && !pawn_found && (code == codes.pawn || code == pawn_theirs)) {
+                    pawn = 1 + (code == pawn_theirs ? 7 : 0) + k;
+                    pawn_found = true;
+                }
+            }
+            row[12 + d] = line;
+            if (d < 2) row[21 + d] = pawn;
+        }
+        int ours = 0, theirs = 0;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int code = square_codes[min(max(jumps[s * 8 + j], 0), SQUARES)];
+            ours += code == codes.knight;
+            theirs += code == codes.knight + codes.theirs;
+        }
+        row[20] = min(ours, 2) * 3 + min(theirs, 2);
+#pragma unroll
+        for (int f = 0; f < FEATURES; f++) rows[s][f] = min(max(row[f] + offsets[f], 0), table_rows - 1);
+    }
+    __syncthreads();
+
+    const int chunks = D / 8;
+    for (int item = tid; item < T * chunks; item += blockDim.x) {
+        const int token = item / chunks, d0 = (item % chunks) * 8;
+        const v8h e = *reinterpret_cast<const v8h*>(embed + (size_t)token_codes[token] * D + d0);
+        const v8h p = *reinterpret_cast<const v8h*>(position + (size_t)token * D + d0);
+        float total[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) total[c] = (float)e[c] + (float)p[c];
+        if (token < SQUARES) {
+            float features[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+            for (int f = 0; f < FEATURES; f++) {
+                const v8h t = *reinterpret_cast<const v8h*>(table + (size_t)rows[token][f] * D + d0);
+#pragma unroll
+                for (int c = 0; c < 8; c++) features[c] = features[c] + (float)t[c];
+            }
+#pragma unroll
+            for (int c = 0; c < 8; c++) total[c] = total[c] + (float)(half_t)features[c];
+        }
+        v8h result;
+#pragma unroll
+        for (int c = 0; c < 8; c++) result[c] = (half_t)total[c];
+        *reinterpret_cast<v8h*>(out + (b * T + token) * D + d0) = result;
+    }
+}
+
+}  // namespace
+
+extern "C" int chess_board_embedding(const void* boards, int code_bytes, const void* rays, const void* jumps, const void* offsets,
+                                     const void* embed, const void* position, const void* table, void* out, int B, int T, int D,
+                                     int embed_rows, int table_rows, int pawn, int knight, int queen, int king, int theirs, int edge,
+                                     int no_piece, void* stream)
+{
+    if (B < 0 || T < SQUARES || T > 128 || D <= 0 || D % 8 != 0 || embed_rows <= 0 || table_rows <= 0)
+        return chess_fail(CHESS_INVALID_SHAPE, "board_embedding takes 64 to 128 tokens and a width a multiple of 8 (T %d, D %d)", T, D);
+    if (code_bytes != 1 && code_bytes != 4 && code_bytes != 8)
+        return chess_fail(CHESS_UNSUPPORTED, "board_embedding reads codes of 1, 4 or 8 bytes, not %d", code_bytes);
+    if (!boards || !rays || !jumps || !offsets || !embed || !position || !table || !out)
+        return chess_fail(CHESS_INVALID_SHAPE, "board_embedding: a required pointer is null");
+    if (!aligned16(embed) || !aligned16(position) || !aligned16(table) || !aligned16(out))
+        return chess_fail(CHESS_MISALIGNED, "board_embedding's 16-byte loads need aligned tables and output");
+    if (B == 0) return CHESS_OK;
+    const Codes codes{pawn, knight, queen, king, theirs, edge, no_piece};
+    hipStream_t s = (hipStream_t)stream;
+    const int* r = (const int*)rays;
+    const int* j = (const int*)jumps;
+    const int* o = (const int*)offsets;
+    const half_t *e = (const half_t*)embed, *p = (const half_t*)position, *t = (const half_t*)table;
+    half_t* y = (half_t*)out;
+    if (code_bytes == 1) {
+        hipLaunchKernelGGL(board_embedding_kernel<uint8_t>, dim3(B), dim3(256), 0, s, (const uint8_t*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+    } else if (code_bytes == 4) {
+        hipLaunchKernelGGL(board_embedding_kernel<int>, dim3(B), dim3(256), 0, s, (const int*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+    } else {
+        hipLaunchKernelGGL(board_embedding_kernel<long long>, dim3(B), dim3(256), 0, s, (const long long*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+    }
+    return launch_status();
+}

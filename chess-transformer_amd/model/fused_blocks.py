@@ -2,9 +2,9 @@
 that the int8 path uses -- the operators chess::template_attention and chess::linear, FusedBlock,
 link_input_mixes, tile_for -- and FusedTransformer, the network the engine calls.
 
-The operators launch the HIP kernels of libchess_hip.so. The heads and the input embedding run as
-torch operations on the GPU, which is the reference's own path on GPUs without its fused ends
-(reference fused_blocks.py:515-529, 863-874; on ROCm fused_ends is never true).
+The operators launch the HIP kernels of libchess_hip.so, the input embedding included (chess::board_embedding, which finds
+the square features from the boards as the reference's board_embedding_kernel does). The heads run as torch operations on
+the GPU, the reference's own path on GPUs without its fused heads (reference fused_blocks.py:863-874).
 """
 from __future__ import annotations
 
@@ -18,9 +18,10 @@ from torch import nn
 from model import hip_kernels
 from model.encoding import NUM_SQUARES, TOKENS_PER_BOARD
 from model.hip_kernels import aligned, check, library_for, pointer, stream_of
-from model.model import ChessTransformer, TransformerBlock
+from model.model import EDGE, KING, KNIGHT, NO_PIECE, PAWN, QUEEN, THEIRS, ChessTransformer, TransformerBlock
 
 LINEAR_DEPTH, GROUP_M = 32, 8
+FEATURE_SLOTS = 23
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
 LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 3)]}
 # positions a launch should reach before a workgroup takes several key/value groups
@@ -60,10 +61,10 @@ def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, 
         raise ValueError(f"template_attention takes {templates_count} templates of 64 x 64, not {tuple(templates.shape)}")
     library = library_for(projected.device)
     projected = aligned(projected)
-    templates = aligned(templates)
+    keyed = keyed_templates(templates, templates_count)
     out = torch.empty(B, T, heads * dv, device=projected.device, dtype=torch.float16)
     groups = groups_per_block or groups_per_workgroup(B, kv_heads)
-    code = library.chess_template_attention(pointer(projected), pointer(templates), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()),
+    code = library.chess_template_attention(pointer(projected), pointer(keyed), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()),
                                             pointer(out), B, T, heads, kv_heads, dq, dv, templates_count, groups, float(eps), 1 / math.sqrt(dq),
                                             stream_of(projected.device))
     check(code, "template_attention")
@@ -81,6 +82,34 @@ def template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain:
 def _(projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, templates_count, eps):
     B, T, _ = projected.shape
     return projected.new_empty(B, T, heads * dv)
+
+
+# by data_ptr: (the templates, their version, the templates used, their key-major copy); the entry holds the templates so that
+# their memory is not another's
+KEYED: dict[int, tuple[torch.Tensor, int, int, torch.Tensor]] = {}
+KEYED_MOST = 64
+KEYED_LOCK = threading.Lock()
+TEMPLATE_SLOTS = 8
+
+
+def keyed_templates(templates: torch.Tensor, templates_count: int) -> torch.Tensor:
+    """keyed[i, j, t] = templates[t, i, j] for t < templates_count, zero up to 8: the kernel reads a query's templates for 4 keys as 64
+    contiguous bytes. Made once per templates and version outside graph recording, as the reference pairs its templates
+    (attention_cuda.py:410-440)."""
+    version = 0 if templates.is_inference() else templates._version
+    found = KEYED.get(templates.data_ptr())
+    if found is not None and found[1] == version and found[2] == templates_count and found[0].shape == templates.shape:
+        return found[3]
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError("template_attention's templates were not seen before the graph recording began (run the model once first)")
+    with torch.no_grad():
+        keyed = torch.zeros(NUM_SQUARES, NUM_SQUARES, TEMPLATE_SLOTS, device=templates.device, dtype=torch.float16)
+        keyed[..., :templates_count] = templates[:templates_count].detach().permute(1, 2, 0)
+    with KEYED_LOCK:
+        KEYED[templates.data_ptr()] = (templates, version, templates_count, keyed)
+        while len(KEYED) > KEYED_MOST:
+            del KEYED[next(iter(KEYED))]
+    return keyed
 
 
 # by data_ptr: (the K x N weight, its version, its N x K copy); the entry holds the weight so that its memory is not another's
@@ -195,25 +224,57 @@ def link_input_mixes(blocks: list[nn.Module]) -> None:
 
 
 def prepare(templates: torch.Tensor) -> None:
-    """Nothing to prepare: the kernels read the templates as the model holds them (the reference paired them, attention_cuda.py:410-440)."""
+    """The key-major templates, made now rather than while a graph records (reference attention_cuda.py:437-440)."""
+    if templates.is_cuda and templates.dtype == torch.float16 and tuple(templates.shape[1:]) == (NUM_SQUARES, NUM_SQUARES):
+        keyed_templates(templates, templates.shape[0])
+
+
+#boards B x T (codes of 1, 4 or 8 bytes): B x T x D. rays 64 x 8 x 8 (each square's squares out along the 8 directions, nearest
+#first, 64 past the edge) and jumps 64 x 8 (its knight jumps), offsets the 23 features' first rows (reference fused_blocks.py:472-491)
+@torch.library.custom_op("chess::board_embedding", mutates_args=())
+def board_embedding(boards: torch.Tensor, rays: torch.Tensor, jumps: torch.Tensor, offsets: torch.Tensor, embed: torch.Tensor, position: torch.Tensor,
+                    table: torch.Tensor) -> torch.Tensor:
+    if boards.dtype not in (torch.uint8, torch.int32, torch.int64):
+        raise ValueError(f"board_embedding reads codes as uint8, int32 or int64, not {boards.dtype}")
+    for tensor, name in ((embed, "embed"), (position, "position"), (table, "table")):
+        if tensor.dtype != torch.float16:
+            raise ValueError(f"board_embedding's {name} is {tensor.dtype}, the kernel takes fp16")
+    for tensor, shape, name in ((rays, (NUM_SQUARES, 8, 8), "rays"), (jumps, (NUM_SQUARES, 8), "jumps"), (offsets, (FEATURE_SLOTS,), "offsets")):
+        if tensor.dtype != torch.int32 or tuple(tensor.shape) != shape:
+            raise ValueError(f"board_embedding's {name} is {tensor.dtype} {tuple(tensor.shape)}, the kernel takes int32 {shape}")
+    boards = boards.contiguous()
+    B, T = boards.shape
+    D = table.shape[1]
+    if embed.shape[1] != D or position.shape[1] != D or position.shape[0] < T:
+        raise ValueError(f"board_embedding: embed {tuple(embed.shape)}, position {tuple(position.shape)} and table {tuple(table.shape)} for {T} tokens")
+    library = library_for(boards.device)
+    embed, position, table = aligned(embed), aligned(position), aligned(table)
+    out = torch.empty(B, T, D, device=boards.device, dtype=torch.float16)
+    code = library.chess_board_embedding(pointer(boards), boards.element_size(), pointer(rays.contiguous()), pointer(jumps.contiguous()),
+                                         pointer(offsets.contiguous()), pointer(embed), pointer(position), pointer(table), pointer(out), B, T, D,
+                                         embed.shape[0], table.shape[0], PAWN, KNIGHT, QUEEN, KING, THEIRS, EDGE, NO_PIECE, stream_of(boards.device))
+    check(code, "board_embedding")
+    return out
+
+
+@board_embedding.register_fake
+def _(boards, rays, jumps, offsets, embed, position, table):
+    return table.new_empty(*boards.shape, table.shape[1])
 
 
 class InputEmbedding(nn.Module):
-    """Token + position embedding plus the square features, summed as the reference's input_embedding kernel sums them
-    (fused_blocks.py:370-393): the features' sum rounded to the table's precision first, then all three in f32."""
+    """Token + position embedding plus the square features (reference fused_blocks.py:494-510), in one kernel that finds each square's
+    feature rows from the board itself: the features' sum rounded to the table's precision first, then all three summed in f32."""
 
     def __init__(self, model: ChessTransformer):
         super().__init__()
         self.embed, self.position_embed, self.features = model.embed, model.position_embed, model.square_features
+        self.register_buffer("rays", F.pad(self.features.rays, (0, 1), value=NUM_SQUARES).int().contiguous(), persistent=False)
+        self.register_buffer("jumps", self.features.knight_jumps.int().contiguous(), persistent=False)
+        self.register_buffer("offsets", self.features.row_offsets.int().contiguous(), persistent=False)
 
     def forward(self, board_state: torch.Tensor) -> torch.Tensor:
-        B = board_state.shape[0]
-        table = self.features.table
-        rows = self.features.indices(board_state) + self.features.row_offsets
-        features = F.embedding_bag(rows.reshape(B * NUM_SQUARES, -1), table.float(), mode="sum").to(table.dtype).reshape(B, NUM_SQUARES, -1)
-        total = self.embed.weight[board_state].float() + self.position_embed.float()
-        total[:, :NUM_SQUARES] += features.float()
-        return total.to(self.embed.weight.dtype)
+        return board_embedding(board_state, self.rays, self.jumps, self.offsets, self.embed.weight, self.position_embed, self.features.table)
 
 
 #logits[i, j] = (W_f x_i + b_f) . (W_t x_j + b_t) / sqrt(d) = a_i . x_j + s_i: from and to as one d x d matmul (a)

@@ -51,12 +51,13 @@ int chess_int8_linear(const void* x, const void* x_scale, const void* w, const v
 int chess_int8_matmul_i32(const void* x, const void* w, void* out, int M, int N, int K, int tile, void* stream);
 
 /* Template attention of B positions of T tokens (64 <= T <= 128): projected[B, T, H*dq | KV*dq | KV*dv | H*tc]
- * fp16, templates[tc, 64, 64] fp16, q_gain/k_gain[dq] fp16 -> out[B, T, H*dv] fp16; scale = 1/sqrt(dq).
+ * fp16, keyed_templates[64, 64, 8] fp16 (keyed[i][j][t] = templates[t][i][j] for t < tc, zero beyond; 16-byte
+ * aligned), q_gain/k_gain[dq] fp16 -> out[B, T, H*dv] fp16; scale = 1/sqrt(dq).
  * groups_per_block key/value groups share a workgroup (any divisor of KV; it changes no bit).
  * Replaces template_attention_cuda (model/attention_cuda.py:97-304, launch :379-391, pointer order
- * projected, templates, q_gain, k_gain, out) and the Triton pair template_bias_kernel +
- * template_attention_kernel (model/fused_blocks.py:35-171). */
-int chess_template_attention(const void* projected, const void* templates, const void* q_gain, const void* k_gain, void* out, int B,
+ * projected, paired templates, q_gain, k_gain, out; templates paired once, :410-440) and the Triton pair
+ * template_bias_kernel + template_attention_kernel (model/fused_blocks.py:35-171). */
+int chess_template_attention(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain, void* out, int B,
                              int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block, float eps,
                              float scale, void* stream);
 
@@ -67,6 +68,17 @@ int chess_template_attention(const void* projected, const void* templates, const
  * linear (:308-318), whose K x N weight the Python layer transposes once. */
 int chess_linear(const void* x, const void* w, const void* bias, const void* residual, const void* original, const void* residual_scale,
                  const void* input_scale, void* out, int M, int N, int K, int gated, int out_dtype, int tile, void* stream);
+
+/* The network's input out[B, T, D] fp16 from boards[B, T] of token codes (code_bytes 1, 4 or 8 each; 64 <= T <= 128):
+ * embed[code] + position[t] (+ the 64 squares' 23 feature rows of table, summed in f32 in slot order and rounded to
+ * fp16), summed in f32. The rows are found from the boards: rays[64][8][8] (each square's squares along the 8 directions,
+ * nearest first, 64 past the edge), jumps[64][8] (its knight jumps, 64 off the board), offsets[23] (each feature's first
+ * row), all int32, and the piece codes given. Rows and codes are clamped into the tables (embed_rows, table_rows).
+ * Replaces board_embedding_kernel / the op board_embedding (model/fused_blocks.py:412-491) and input_embedding
+ * (:376-409) with SquareFeatures.indices (model/model.py:128-174). */
+int chess_board_embedding(const void* boards, int code_bytes, const void* rays, const void* jumps, const void* offsets, const void* embed,
+                          const void* position, const void* table, void* out, int B, int T, int D, int embed_rows, int table_rows, int pawn,
+                          int knight, int queen, int king, int theirs, int edge, int no_piece, void* stream);
 
 /* Fills table[0..6] with hipSetDevice, hipMemcpyAsync, hipGraphLaunch, hipEventRecord, hipEventSynchronize,
  * hipStreamSynchronize, hipGetErrorString: the address table of engine/cuda_runtime.py:17-49 (CudaRuntime.CALLS

@@ -4,6 +4,7 @@ Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use this mo
 state_dict (the reference's checkpoint format, model/checkpoint.py:22-23) and never imports the product.
 
   square_feature_rows  model/model.py:128-174 (SquareFeatures.indices), by walking the board square by square
+  input_embedding      model/fused_blocks.py:370-393 (input_embedding_kernel): the features summed in f32 in slot order
   fp32_forward         model/model.py:71-99, 245-270: the reference's CPU path (engine/inference.py:274-278)
   int8_forward         engine/inference.py:238-272 + model/int8_blocks.py:254-298 + model/fused_blocks.py:325-363:
                        the fp16 network (stream scaled by 1/16) with int8 blocks from int8_ops, and the fp32 heads
@@ -233,6 +234,20 @@ def _fp16_block(half: dict, layer: int, x: np.ndarray, templates: np.ndarray, or
     return int8_ops.linear(hidden, down, residual=x, original=original, residual_scale=next_scales[0], input_scale=next_scales[1])
 
 
+def input_embedding(boards: np.ndarray, embed: np.ndarray, position: np.ndarray, table: np.ndarray) -> np.ndarray:
+    """fp16 B x T x D: f16((f32(embed[code]) + f32(position[t])) + f32(f16(features))), features the square's 23 rows summed in f32
+    one after another in slot order (model/fused_blocks.py:383-393 of the reference: store_embedding and the kernel's loop)."""
+    boards = np.asarray(boards).astype(np.int64)
+    rows = square_feature_rows(boards) + ROW_OFFSETS
+    table = np.asarray(table, dtype=np.float16).astype(np.float32)
+    features = np.zeros((len(boards), NUM_SQUARES, table.shape[1]), dtype=np.float32)
+    for slot in range(rows.shape[-1]):
+        features = features + table[rows[..., slot]]
+    total = np.asarray(embed, dtype=np.float16).astype(np.float32)[boards] + np.asarray(position, dtype=np.float16).astype(np.float32)[:boards.shape[1]]
+    total[:, :NUM_SQUARES] = total[:, :NUM_SQUARES] + features.astype(np.float16).astype(np.float32)
+    return total.astype(np.float16)
+
+
 @torch.no_grad()
 def int8_forward(state: dict, settings: dict, weights: dict, boards: torch.Tensor, output_scale: float = 1 / 16) -> tuple[torch.Tensor, torch.Tensor]:
     """The int8 network (engine/inference.py:267-272): the layers in weights as Int8Blocks, the rest fp16 blocks, input mixes linked
@@ -241,11 +256,7 @@ def int8_forward(state: dict, settings: dict, weights: dict, boards: torch.Tenso
     heads = settings.get("n_heads", 4)
     boards = boards.cpu().long()
     half = _fp16_state(state, output_scale)
-    features = torch.from_numpy(square_feature_rows(boards.numpy()) + ROW_OFFSETS)
-    summed = half["square_features.table"].float()[features].sum(-2).half().float()
-    embed = half["embed.weight"].float()[boards] + half["position_embed"].float()
-    embed[:, :NUM_SQUARES] += summed
-    x = original = embed.half().numpy()
+    x = original = input_embedding(boards.numpy(), _np(half, "embed.weight"), _np(half, "position_embed"), _np(half, "square_features.table"))
     templates = _np(half, "templates")
     kinds = ["int8" if layer in weights else "fp16" for layer in range(_layers(state))]
     for layer, kind in enumerate(kinds):

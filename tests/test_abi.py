@@ -68,6 +68,7 @@ def test_refused_shapes_come_back_as_codes(library):
     assert attention(1, 70, 8, 8, 64, 48, 8, 1) == hip_kernels.UNSUPPORTED             # value width
     assert attention(1, 70, 8, 8, 64, 64, 9, 1) == hip_kernels.UNSUPPORTED             # 9 templates
     assert attention(1, 70, 8, 8, 64, 64, 8, 3) == hip_kernels.INVALID_SHAPE           # 3 groups a workgroup for 8
+    assert library.chess_template_attention(16, 8, 16, 16, 16, 1, 70, 8, 8, 64, 64, 8, 1, 1e-5, 0.125, None) == hip_kernels.MISALIGNED
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
 

@@ -267,3 +267,23 @@ def test_the_runtime_table_copies_and_launches(device):
     runtime.check(runtime.memcpy(back.data_ptr(), on_device.data_ptr(), 1024, DEVICE_TO_HOST, stream.cuda_stream), "copy out")
     runtime.check(runtime.stream_synchronize(stream.cuda_stream), "synchronize")
     assert torch.equal(back, host)
+
+
+@pytest.mark.parametrize("d_model", [128, 512])
+@pytest.mark.parametrize("codes", [torch.uint8, torch.int64])
+def test_the_board_embedding_is_the_oracles_to_the_bit(device, d_model, codes):
+    """chess::board_embedding finds every square's 23 feature rows from the board and sums them in slot order, as the oracle does."""
+    model = ChessTransformer(d_model=d_model, num_layers=1, n_heads=4).eval()
+    torch.manual_seed(d_model)
+    with torch.no_grad():
+        for tensor in (model.embed.weight, model.position_embed, model.square_features.table):
+            tensor.normal_()
+    model = model.half()
+    boards = random_boards(37, seed=d_model)
+    boards[0, :64] = 0                                   # no king or queen: the offsets take NO_PIECE
+    boards[1, :64] = torch.tensor([6, 12, 5, 11] + [1, 7] * 30)
+    state = {name: value.numpy().copy() for name, value in model.state_dict().items()}
+    embedding = fused_blocks.InputEmbedding(model).to(device)
+    out = embedding(boards.to(device, codes))
+    expected = oracle_network.input_embedding(boards.numpy(), state["embed.weight"], state["position_embed"], state["square_features.table"])
+    assert out.dtype == torch.float16 and torch.equal(out.cpu(), torch.from_numpy(expected))

@@ -168,6 +168,31 @@ def test_the_square_features_of_a_known_position():
     assert features[A1, 4 + 3] == 13 and features[A1, 12 + 3] == 0
 
 
+def test_the_input_embedding_is_the_models():
+    """The slot-order f32 sum of the feature rows, rounded to fp16, plus the token and position embeddings: the model's embedding in
+    f64 (model/model.py:245-250 of the reference) to within the fp16 roundings."""
+    model = small_state({"d_model": 64, "num_layers": 1, "n_heads": 4})
+    boards = random_boards(6, seed=3)
+    boards[0] = torch.tensor(KNOWN)
+    with torch.no_grad():
+        model.embed.weight.normal_()
+        model.position_embed.normal_()
+        double = model.double()
+        expected = (double.embed(boards) + double.position_embed + F.pad(double.square_features(boards), (0, 0, 0, 6))).numpy()
+    half = {name: value.half().numpy() for name, value in model.state_dict().items()}
+    found = network.input_embedding(boards.numpy(), half["embed.weight"], half["position_embed"], half["square_features.table"])
+    assert found.dtype == np.float16
+    assert np.allclose(found.astype(np.float64), expected, atol=4e-3, rtol=4e-3)
+    # one row changed by a known amount moves exactly the squares that use it
+    table = half["square_features.table"].copy()
+    row = network.square_feature_rows(boards.numpy()[:1])[0, E4, 20] + network.ROW_OFFSETS[20]
+    table[row] = 0
+    moved = network.input_embedding(boards.numpy()[:1], half["embed.weight"], half["position_embed"], table)
+    uses = (network.square_feature_rows(boards.numpy()[:1])[0] + network.ROW_OFFSETS == row).any(-1)
+    changed = (moved[0] != found[0]).any(-1)
+    assert changed[:64][~uses].sum() == 0 and changed[E4]
+
+
 def small_state(settings, seed=0):
     from model.model import ChessTransformer
     torch.manual_seed(seed)
