@@ -16,6 +16,8 @@
 // 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B operand, so the probabilities
 // never leave registers. A lane keeps its query's templates for its 16 square keys in registers across
 // the heads, as f16 pairs: the bias of a key is 4 v_dot2_f32_f16 of them with the head's coefficients.
+// Attention is held to a tolerance, not to bits: the norms take the hardware reciprocal square root, sums
+// of squares are v_dot2_f32_f16 of the fp16 pairs, and the softmax's exponent is one fma.
 #include "chess_common.h"
 
 namespace {
@@ -24,21 +26,65 @@ constexpr int MAX_TEMPLATES = 8;
 constexpr float LOG2E = 1.44269504f;
 
 typedef __fp16 h2 __attribute__((ext_vector_type(2)));
+#define LDS_SPACE __attribute__((address_space(3)))
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 
 DEVICE float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
+}
+
+// the sum of squares of 8 halves
+DEVICE float squares8(const v8h& v, float c) {
+    const uint4 w = __builtin_bit_cast(uint4, v);
+    return dot2(w.w, w.w, dot2(w.z, w.z, dot2(w.y, w.y, dot2(w.x, w.x, c))));
 }
 
 // TILES: key tiles of 16 the instantiation holds (T <= 16 TILES)
 template <int DQP, int DV, int TILES>
 struct Layout {
     static constexpr int STEPS = (TILES + 1) / 2;     // 32-key steps of P V
-    static constexpr int KEYS = TILES * 16;           // keys staged
-    static constexpr int VKEYS = STEPS * 32;          // value keys staged (zero past T)
-    static constexpr int K_ROW = DQP + 8;             // halves a staged key, padded against bank conflicts
-    static constexpr int V_ROW = VKEYS + 8;           // halves a staged value column: 8 mod 16, so that the
+    static constexpr int KEYS = TILES * 16;           // keys (and queries) staged
+    static constexpr int VKEYS = STEPS * 32;          // value keys staged (P is zero past T)
+    static constexpr int K_ROW = DQP + 8;             // halves a normalised key, padded against bank conflicts
+    static constexpr int V_ROW = VKEYS + 8;           // halves a transposed value column: 8 mod 16, so that the
                                                       // transposing writes of key pairs spread over the banks
+    static constexpr int KC = DQP / 8, VC = DV / 8;   // 16-byte chunks a raw key (query) row, a raw value row
+    // LDS in bytes: normalised keys, transposed values, raw keys, raw values, then two buffers of raw queries
+    static constexpr int KEYS_BYTES = KEYS * K_ROW * 2;
+    static constexpr int VALUES_BYTES = DV * V_ROW * 2;
+    static constexpr int RAW_K_BYTES = KEYS * DQP * 2;
+    static constexpr int RAW_V_BYTES = VKEYS * DV * 2;
+    static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
+    static constexpr int FIXED_BYTES = KEYS_BYTES + VALUES_BYTES + RAW_K_BYTES + RAW_V_BYTES;
+    static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * RAW_Q_BYTES; }
 };
+
+// Raw rows are DMA'd 64 16-byte chunks an instruction, the chunks of a row in a swizzled order: chunk c of row r
+// sits in slot r * CH + (c ^ swizzle(r)), which puts the 16 rows an MFMA operand group reads (one chunk each) in
+// 16 different 16-byte bank groups.
+// Every wavefront's LDS writes are done and visible; unlike __syncthreads, the DMA loads in flight go on.
+DEVICE void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt(0xC07F);   // lgkmcnt(0), vmcnt and expcnt left alone
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int CH> DEVICE int swizzle(int row) { return CH >= 16 ? row % CH : (row / (16 / CH)) % CH; }
+template <int CH> DEVICE int raw_slot(int row, int chunk) { return row * CH + (chunk ^ swizzle<CH>(row)); }
+
+// Issue this wavefront's share of the DMA of rows [0, rows) of a raw block: row r's 16-byte chunk c from
+// source + min(r, last) * stride + 8 c halves into slot raw_slot(r, c). Rows past last read row last again (their
+// values are masked or multiplied by zero later), so every address is inside the projected rows.
+template <int CH>
+DEVICE void dma_rows(LDS_SPACE int8_t* raw, const half_t* source, int rows, int last, int stride, int wave, int waves, int lane) {
+    const int instructions = rows * CH / 64;
+    for (int i = wave; i < instructions; i += waves) {
+        const int slot = i * 64 + lane, row = slot / CH, chunk = (slot % CH) ^ swizzle<CH>(row);
+        const half_t* from = source + (size_t)min(row, last) * stride + chunk * 8;
+        __builtin_amdgcn_global_load_lds((const void*)from, (LDS_SPACE void*)(raw + i * 1024), 16, 0, 0);
+    }
+}
 
 template <int DQP, int DV, int TILES>
 __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
@@ -47,31 +93,59 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
     int groups_per_block, float eps, float scale)
 {
     typedef Layout<DQP, DV, TILES> L;
-    __shared__ __align__(16) half_t keys[L::KEYS * L::K_ROW];
-    __shared__ __align__(16) half_t values[DV * L::V_ROW];
+    constexpr int KC = L::KC, VC = L::VC;
+    extern __shared__ __align__(16) int8_t lds[];
+    half_t* keys = (half_t*)lds;
+    half_t* values = (half_t*)(lds + L::KEYS_BYTES);
+    LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)(lds + L::KEYS_BYTES + L::VALUES_BYTES);
+    LDS_SPACE int8_t* raw_v = raw_k + L::RAW_K_BYTES;
+    LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES;     // [2][per_kv][KEYS * DQP halves]
 
     const int lane = threadIdx.x & 63, slab = threadIdx.x >> 6;
-    const int threads = blockDim.x;
+    const int threads = blockDim.x, waves = threads / 64;
     const int b = blockIdx.y;
     const int tiles = (T + 15) / 16;            // key tiles of the scores
+    const int steps = (tiles + 1) / 2;
     const int width = heads * dq + kv_heads * dq + kv_heads * DV + heads * templates_count;
     const int k_offset = heads * dq, v_offset = k_offset + kv_heads * dq, c_offset = v_offset + kv_heads * DV;
     const int per_kv = heads / kv_heads;
     const half_t* board = projected + (size_t)b * T * width;
+    const int head_bytes = L::RAW_Q_BYTES;
 
     const int col = lane & 15, quad = lane >> 4;
     const int query = slab * 16 + col;
     const bool query_ok = query < T;
     const bool square_query = query < 64;
 
+    // the first group's rows on their way while the templates and gains load
+    auto dma_group = [&](int group, bool kv, bool q, int buffer) {
+        if (kv) {
+            dma_rows<KC>(raw_k, board + k_offset + group * dq, tiles * 16, T - 1, width, slab, waves, lane);
+            dma_rows<VC>(raw_v, board + v_offset + group * DV, steps * 32, T - 1, width, slab, waves, lane);
+        }
+        if (q) {
+            for (int hi = 0; hi < per_kv; hi++)
+                dma_rows<KC>(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, tiles * 16, T - 1, width,
+                             slab, waves, lane);
+        }
+    };
+    dma_group(blockIdx.x * groups_per_block, true, true, 0);
+
     // this lane's templates: keyed[query][16 kt + 4 quad + r][0..7], 4 f16 pairs a key
+    // (loaded unconditionally from clamped places, then zeroed, so that the loads issue together)
     uint4 pairs[4][4];
+    const int template_query = min(query, 63);
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
         for (int r = 0; r < 4; r++)
-            pairs[kt][r] = square_query ? *reinterpret_cast<const uint4*>(keyed + ((size_t)query * 64 + kt * 16 + quad * 4 + r) * MAX_TEMPLATES)
-                                        : uint4{0, 0, 0, 0};
+            pairs[kt][r] = *reinterpret_cast<const uint4*>(keyed + ((size_t)template_query * 64 + kt * 16 + quad * 4 + r) * MAX_TEMPLATES);
+    if (!square_query) {
+#pragma unroll
+        for (int kt = 0; kt < 4; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) pairs[kt][r] = uint4{0, 0, 0, 0};
+    }
 
     half_t q_gains[DQP / 32][8];
 #pragma unroll
@@ -79,100 +153,98 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int d = ks * 32 + quad * 8 + e;
-            q_gains[ks][e] = d < dq ? q_gain[d] : (half_t)0.0f;
+            const half_t gain = q_gain[min(d, dq - 1)];
+            q_gains[ks][e] = d < dq ? gain : (half_t)0.0f;
         }
+    // the key gains of the chunk this thread normalises (chunk threadIdx.x % KC of every key it takes)
+    half_t k_gains[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+        const int d = (threadIdx.x % KC) * 8 + e;
+        const half_t gain = k_gain[min(d, dq - 1)];
+        k_gains[e] = d < dq ? gain : (half_t)0.0f;
+    }
+    const float inverse_dq = 1.0f / (float)dq;
 
     for (int gi = 0; gi < groups_per_block; gi++) {
         const int group = blockIdx.x * groups_per_block + gi;
-        if (gi > 0) __syncthreads();   // every wavefront is done with the previous group's keys and values
+        const int buffer = gi & 1;
+        // this group's raw rows have landed (this wavefront's DMA), and every wavefront is past the previous group
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (gi + 1 < groups_per_block) dma_group(group + 1, false, true, buffer ^ 1);
 
-        // keys: 8-half chunks, CH = DQP / 8 adjacent lanes a key, normalised with the gain
-        constexpr int CH = DQP / 8;
-        for (int item = threadIdx.x; item < tiles * 16 * CH; item += threads) {
-            const int key = item / CH, c = item % CH;
-            float v[8];
-            if (key < T && c * 8 < dq) {
-                const v8h raw = *reinterpret_cast<const v8h*>(board + (size_t)key * width + k_offset + group * dq + c * 8);
+        // keys, normalised with the gain: a thread a 16-byte chunk, KC adjacent lanes a key
+        for (int item = threadIdx.x; item < tiles * 16 * KC; item += threads) {
+            const int key = item / KC, c = item % KC;
+            v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(raw_k + raw_slot<KC>(key, c) * 16);
+            if (c * 8 >= dq) raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+            float squares = squares8(raw, 0.0f);
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (float)raw[e];
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = 0.0f;
-            }
-            float squares = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; e++) squares += v[e] * v[e];
-#pragma unroll
-            for (int offset = 1; offset < CH; offset <<= 1) squares += __shfl_xor(squares, offset, 64);
-            const float inverse = 1.0f / __builtin_sqrtf(squares / (float)dq + eps);
+            for (int offset = 1; offset < KC; offset <<= 1) squares += __shfl_xor(squares, offset, 64);
+            const float inverse = __builtin_amdgcn_rsqf(squares * inverse_dq + eps);
             v8h normed;
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const int d = c * 8 + e;
-                normed[e] = (half_t)(d < dq ? (v[e] * inverse) * (float)k_gain[d] : 0.0f);
-            }
+            for (int e = 0; e < 8; e++) normed[e] = (half_t)(((float)raw[e] * inverse) * (float)k_gains[e]);
             *reinterpret_cast<v8h*>(keys + key * L::K_ROW + c * 8) = normed;
         }
-        // values, transposed to [d][key] a key pair at a time (4-byte writes); keys past T are zero
-        constexpr int VC = DV / 8, KP = L::VKEYS / 2;
-        for (int item = threadIdx.x; item < KP * VC; item += threads) {
-            const int kp = item % KP, c = item / KP, key = 2 * kp;
-            v8h first = v8h{0, 0, 0, 0, 0, 0, 0, 0}, second = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-            if (key < T) first = *reinterpret_cast<const v8h*>(board + (size_t)key * width + v_offset + group * DV + c * 8);
-            if (key + 1 < T) second = *reinterpret_cast<const v8h*>(board + (size_t)(key + 1) * width + v_offset + group * DV + c * 8);
-            const uint4 lo = __builtin_bit_cast(uint4, first), hi = __builtin_bit_cast(uint4, second);
-            const uint32_t lo_words[4] = {lo.x, lo.y, lo.z, lo.w}, hi_words[4] = {hi.x, hi.y, hi.z, hi.w};
+        // values, transposed to [d][key] a key pair at a time (4-byte writes)
+        for (int item = threadIdx.x; item < steps * 16 * VC; item += threads) {
+            const int kp = item % (steps * 16), c = item / (steps * 16), key = 2 * kp;
+            const v4u lo = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key, c) * 16);
+            const v4u hi = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key + 1, c) * 16);
+            const uint32_t lo_words[4] = {lo[0], lo[1], lo[2], lo[3]}, hi_words[4] = {hi[0], hi[1], hi[2], hi[3]};
 #pragma unroll
             for (int e = 0; e < 8; e++) {
                 // element e of a row is half e % 2 of its word e / 2
-                const uint32_t a = e % 2 ? lo_words[e / 2] >> 16 : lo_words[e / 2] & 0xFFFFu;
-                const uint32_t b = e % 2 ? hi_words[e / 2] >> 16 : hi_words[e / 2] & 0xFFFFu;
-                *reinterpret_cast<uint32_t*>(values + (c * 8 + e) * L::V_ROW + key) = a | (b << 16);
+                const uint32_t first = e % 2 ? lo_words[e / 2] >> 16 : lo_words[e / 2] & 0xFFFFu;
+                const uint32_t second = e % 2 ? hi_words[e / 2] >> 16 : hi_words[e / 2] & 0xFFFFu;
+                *reinterpret_cast<uint32_t*>(values + (c * 8 + e) * L::V_ROW + key) = first | (second << 16);
             }
         }
-        __syncthreads();
+        lds_barrier();
+        // the raw keys and values are read: the next group's come in while this one's heads run
+        if (gi + 1 < groups_per_block) dma_group(group + 1, true, false, 0);
 
         for (int hi = 0; hi < per_kv; hi++) {
             const int head = group * per_kv + hi;
-            // the query row's fragment of B: lane holds dq columns ks * 32 + 8 quad .. + 8
-            float qv[DQP / 32][8];
-            float squares = 0.0f;
-#pragma unroll
-            for (int ks = 0; ks < DQP / 32; ks++) {
-                const int d0 = ks * 32 + quad * 8;
-                if (query_ok && d0 < dq) {
-                    const v8h raw = *reinterpret_cast<const v8h*>(board + (size_t)query * width + head * dq + d0);
-#pragma unroll
-                    for (int e = 0; e < 8; e++) qv[ks][e] = (float)raw[e];
-                } else {
-#pragma unroll
-                    for (int e = 0; e < 8; e++) qv[ks][e] = 0.0f;
-                }
-#pragma unroll
-                for (int e = 0; e < 8; e++) squares += qv[ks][e] * qv[ks][e];
-            }
             // this query's template coefficients for the head, as f16 pairs (zero past templates_count)
-            uint4 coefficients = uint4{0, 0, 0, 0};
-            if (square_query) {
-                const half_t* from = board + (size_t)query * width + c_offset + head * templates_count;
+            uint4 coefficients;
+            {
+                const half_t* from = board + (size_t)min(query, 63) * width + c_offset + head * templates_count;
                 if (templates_count == MAX_TEMPLATES) {
                     coefficients = *reinterpret_cast<const uint4*>(from);
                 } else {
                     uint16_t c[MAX_TEMPLATES];
 #pragma unroll
-                    for (int t = 0; t < MAX_TEMPLATES; t++) c[t] = t < templates_count ? __builtin_bit_cast(uint16_t, from[t]) : (uint16_t)0;
+                    for (int t = 0; t < MAX_TEMPLATES; t++) {
+                        const uint16_t value = __builtin_bit_cast(uint16_t, from[min(t, max(templates_count - 1, 0))]);
+                        c[t] = t < templates_count ? value : (uint16_t)0;
+                    }
                     coefficients = uint4{c[0] | ((uint32_t)c[1] << 16), c[2] | ((uint32_t)c[3] << 16), c[4] | ((uint32_t)c[5] << 16),
                                          c[6] | ((uint32_t)c[7] << 16)};
                 }
+                if (!square_query) coefficients = uint4{0, 0, 0, 0};
+            }
+            // the query row's fragment of B: lane holds dq columns ks * 32 + 8 quad .. + 8
+            const LDS_SPACE int8_t* queries = raw_q + (buffer * per_kv + hi) * head_bytes;
+            v8h qv[DQP / 32];
+            float squares = 0.0f;
+#pragma unroll
+            for (int ks = 0; ks < DQP / 32; ks++) {
+                const int c = ks * 4 + quad;
+                qv[ks] = *reinterpret_cast<const LDS_SPACE v8h*>(queries + raw_slot<KC>(query, c) * 16);
+                if (c * 8 >= dq) qv[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+                squares = squares8(qv[ks], squares);
             }
             squares += __shfl_xor(squares, 16, 64);
             squares += __shfl_xor(squares, 32, 64);
-            const float q_inverse = 1.0f / __builtin_sqrtf(squares / (float)dq + eps);
+            const float q_inverse = __builtin_amdgcn_rsqf(squares * inverse_dq + eps);
             v8h qf[DQP / 32];
 #pragma unroll
             for (int ks = 0; ks < DQP / 32; ks++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)((qv[ks][e] * q_inverse) * (float)q_gains[ks][e]);
+                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)(((float)qv[ks][e] * q_inverse) * (float)q_gains[ks][e]);
 
             // S^T tiles: lane holds s[query][16 kt + 4 quad + r]
             float s[2 * L::STEPS][4];
@@ -201,24 +273,25 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
                         bias = dot2(coefficients.w, pairs[kt][r].w, bias);
                         value += (float)(half_t)bias;
                     }
-                    s[kt][r] = key < T ? value : -__builtin_inff();
+                    s[kt][r] = kt < 4 || key < T ? value : -__builtin_inff();
                     top = fmaxf(top, s[kt][r]);
                 }
             }
             top = fmaxf(top, __shfl_xor(top, 16, 64));
             top = fmaxf(top, __shfl_xor(top, 32, 64));
             float total = 0.0f;
+            const float offset = -top * LOG2E;
 #pragma unroll
             for (int kt = 0; kt < 2 * L::STEPS; kt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const float p = kt < TILES ? __builtin_amdgcn_exp2f((s[kt][r] - top) * LOG2E) : 0.0f;
+                    const float p = kt < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], LOG2E, offset)) : 0.0f;
                     s[kt][r] = p;
                     total += p;
                 }
             total += __shfl_xor(total, 16, 64);
             total += __shfl_xor(total, 32, 64);
-            const float inverse_total = 1.0f / total;
+            const float inverse_total = __builtin_amdgcn_rcpf(total);
 
             // O^T = V^T P^T over 32-key steps: position e of both operands is key 32 st + 16 (e / 4) + 4 quad + e % 4
             v4f o[DV / 16];
@@ -259,10 +332,18 @@ template <int DQP, int DV, int TILES>
 int launch(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
            int kv_heads, int dq, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
+    typedef Layout<DQP, DV, TILES> L;
+    const int bytes = L::bytes(heads / kv_heads);
+    if (bytes > 160 * 1024)
+        return chess_fail(CHESS_UNSUPPORTED, "template_attention would stage %d bytes of LDS for %d heads a key/value head", bytes, heads / kv_heads);
+    auto kernel = template_attention_kernel<DQP, DV, TILES>;
+    if (bytes > 65536) {
+        const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (allowed != hipSuccess) return (int)allowed;
+    }
     const dim3 grid(kv_heads / groups_per_block, B), block(64 * ((T + 15) / 16));
-    hipLaunchKernelGGL((template_attention_kernel<DQP, DV, TILES>), grid, block, 0, stream, (const half_t*)projected, (const half_t*)keyed,
-                       (const half_t*)q_gain, (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block,
-                       eps, scale);
+    hipLaunchKernelGGL(kernel, grid, block, bytes, stream, (const half_t*)projected, (const half_t*)keyed, (const half_t*)q_gain,
+                       (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale);
     return launch_status();
 }
 
