@@ -75,8 +75,9 @@ DEVICE float wave_max(float v) {
 // workgroups to the 8 XCDs round-robin, and each XCD has its own L2.
 DEVICE int xcd_local_tile(int wg, int tiles) {
     constexpr int XCDS = 8;
-    if (tiles % XCDS != 0) return wg;
-    return (wg % XCDS) * (tiles / XCDS) + wg / XCDS;
+    // workgroups go to the XCDs in turn: XCD x gets the contiguous tiles [x q + min(x, r), ...), q + (x < r) of them
+    const int q = tiles / XCDS, r = tiles % XCDS, x = wg % XCDS;
+    return x * q + min(x, r) + wg / XCDS;
 }
 
 // Host-side launch-result check shared by the entry points.

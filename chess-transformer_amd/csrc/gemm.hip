@@ -75,20 +75,34 @@ template <> struct Mfma<half_t> {
 
 DEVICE v4h quad_halves(const half_t* p) { return *reinterpret_cast<const v4h*>(p); }
 
+// outputs are streamed (non-temporal stores), so that they do not push the operands out of L2
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
 template <> DEVICE void store_eight<half_t>(half_t* to, const float (&v)[8]) {
-    *reinterpret_cast<v8h*>(to) = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+    const v8h eight = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+    __builtin_nontemporal_store(eight, reinterpret_cast<v8h*>(to));
 }
 template <> DEVICE void store_eight<bf16_t>(bf16_t* to, const float (&v)[8]) {
-    uint32_t packed[4];
+    v4u packed;
 #pragma unroll
     for (int c = 0; c < 4; c++) packed[c] = (uint32_t)bf16_from_float(v[2 * c]).bits | ((uint32_t)bf16_from_float(v[2 * c + 1]).bits << 16);
-    *reinterpret_cast<uint4*>(to) = uint4{packed[0], packed[1], packed[2], packed[3]};
+    __builtin_nontemporal_store(packed, reinterpret_cast<v4u*>(to));
 }
 template <> DEVICE void store_eight<float>(float* to, const float (&v)[8]) {
-    *reinterpret_cast<float4*>(to) = float4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<float4*>(to + 4) = float4{v[4], v[5], v[6], v[7]};
+    __builtin_nontemporal_store(v4f{v[0], v[1], v[2], v[3]}, reinterpret_cast<v4f*>(to));
+    __builtin_nontemporal_store(v4f{v[4], v[5], v[6], v[7]}, reinterpret_cast<v4f*>(to + 4));
 }
+
+template <typename OutT> DEVICE void stage_four(OutT* to, const float (&v)[4]);
+template <> DEVICE void stage_four<half_t>(half_t* to, const float (&v)[4]) {
+    *reinterpret_cast<v4h*>(to) = v4h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+template <> DEVICE void stage_four<bf16_t>(bf16_t* to, const float (&v)[4]) {
+    const uint32_t lo = (uint32_t)bf16_from_float(v[0]).bits | ((uint32_t)bf16_from_float(v[1]).bits << 16);
+    const uint32_t hi = (uint32_t)bf16_from_float(v[2]).bits | ((uint32_t)bf16_from_float(v[3]).bits << 16);
+    *reinterpret_cast<uint2*>(to) = uint2{lo, hi};
+}
+template <typename OutT> DEVICE void stage_four(OutT*, const float (&)[4]) {}
 
 // s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding)
 constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
@@ -107,7 +121,7 @@ template <int OUTSTANDING> DEVICE void stage_barrier() {
     bare_barrier();
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
 __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
 {
@@ -203,9 +217,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
     bare_barrier();
 
-    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the f32 tile in LDS ([BM][BN + 4]).
+    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the tile in LDS: in f32 ([BM][BN + 4])
+    // when phase 2 still adds to it, else (PACKED) already rounded to the 16-bit output ([BM][BN + 8]).
     // A fragment's lane holds row lane % 32 and, in register 4 q + r, column 8 q + 4 (lane / 32) + r.
     float* staged = (float*)lds;
+    OutT* packed = (OutT*)lds;
     const bool quads = N % 4 == 0;
 #pragma unroll
     for (int i = 0; i < FM; i++) {
@@ -262,7 +278,14 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                         }
                     }
                 }
-                *reinterpret_cast<float4*>(staged + m_local * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
+                if constexpr (PACKED) {
+                    // the f32 value is what rounds: keep its last multiply out of the conversion (one rounding, not two)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) asm volatile("" : "+v"(value[r]));
+                    stage_four<OutT>(packed + m_local * (BN + 8) + n_local, value);
+                } else {
+                    *reinterpret_cast<float4*>(staged + m_local * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
+                }
             }
     }
     __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
@@ -283,6 +306,18 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         const int m = m0 + m_local, n = n0 + n_local;
         if (m >= M || n >= N) continue;
         const size_t at = (size_t)m * N + n;
+        if constexpr (PACKED) {
+            const uint4 eight = *reinterpret_cast<const uint4*>(packed + m_local * (BN + 8) + n_local);
+            if (vectors) {
+                __builtin_nontemporal_store(__builtin_bit_cast(v4u, eight), reinterpret_cast<v4u*>(out + at));
+            } else {
+                const OutT* values = reinterpret_cast<const OutT*>(&eight);
+#pragma unroll
+                for (int c = 0; c < 8; c++)
+                    if (n + c < N) out[at + c] = values[c];
+            }
+            continue;
+        }
         const float4 lo = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local);
         const float4 hi = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local + 4);
         float value[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
@@ -331,11 +366,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     }
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
 int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
-    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = BM * (BN + 4) * 4;
+    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = PACKED ? BM * (BN + 8) * 2 : BM * (BN + 4) * 4;
     constexpr int BYTES = RING > STAGING ? RING : STAGING;
-    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT>;
+    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED>;
     if (BYTES > 65536) {
         static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
         if (allowed != hipSuccess) return (int)allowed;
@@ -345,25 +380,38 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
     return launch_status();
 }
 
-constexpr int TILES = 6;
+constexpr int TILES = 9;
 
 // The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
-// 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4). 0 picks by the launch's size.
+// 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
+// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3). 0 picks by the launch's size.
+template <typename In, int NB, typename OutT, bool PACKED>
+int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    switch (tile) {
+        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 6: return launch<In, 256, 64, 4, 1, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        default: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+    }
+}
+
+// A 16-bit output with nothing left to add is staged already rounded (half the LDS of the f32 staging).
 template <typename In, int NB, typename OutT>
 int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     if (tile == 0) {
         const long large = (long)((M + 255) / 256) * ((N + 127) / 128);
         tile = large >= 512 ? 4 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
     }
-    switch (tile) {
-        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
-        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
-        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
-        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT>(x, w, out, e, M, N, K, stream);
-        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT>(x, w, out, e, M, N, K, stream);
-        default: return launch<In, 256, 64, 4, 1, NB, 4, OutT>(x, w, out, e, M, N, K, stream);
+    if constexpr (sizeof(OutT) == 2) {
+        if (!(e.flags & (EPI_RESIDUAL | EPI_MIX))) return by_tile<In, NB, OutT, true>(x, w, out, e, M, N, K, tile, stream);
     }
+    return by_tile<In, NB, OutT, false>(x, w, out, e, M, N, K, tile, stream);
 }
 
 int check(const void* x, const void* w, void* out, int M, int N, int K, int depth, int tile, const char* what) {
