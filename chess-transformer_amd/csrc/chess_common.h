@@ -57,17 +57,25 @@ DEVICE float silu_fast(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f));
 }
 
+// lane ^ 1 and lane ^ 2 by DPP quad permutes (no LDS round trip): quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]
+DEVICE float lane_xor1(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); }
+DEVICE float lane_xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)); }
+
 // xor butterflies over the 64 lanes of a wavefront: every lane ends with the same bits,
 // the balanced tree of adjacent lane pairs (a + b == b + a bitwise).
 DEVICE float wave_sum(float v) {
+    v = v + lane_xor1(v);
+    v = v + lane_xor2(v);
 #pragma unroll
-    for (int offset = 1; offset < 64; offset <<= 1) v = v + __shfl_xor(v, offset, 64);
+    for (int offset = 4; offset < 64; offset <<= 1) v = v + __shfl_xor(v, offset, 64);
     return v;
 }
 
 DEVICE float wave_max(float v) {
+    v = fmaxf(v, lane_xor1(v));
+    v = fmaxf(v, lane_xor2(v));
 #pragma unroll
-    for (int offset = 1; offset < 64; offset <<= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
+    for (int offset = 4; offset < 64; offset <<= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
     return v;
 }
 
@@ -89,4 +97,4 @@ static inline int launch_status() {
 // Records a message for chess_last_error() and returns code.
 int chess_fail(int code, const char* format, ...);
 
-static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+__host__ __device__ static inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }

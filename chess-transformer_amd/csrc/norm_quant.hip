@@ -3,125 +3,156 @@
 //   [mixed = f16((x * rs) + (original * is))]
 //   y = (x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain
 //   absmax = max(max |y|, 1e-20);  q = rint(y * (127 / absmax));  scale = absmax / 127
-// One wavefront per row; a lane holds C = next_pow2(D) / 64 contiguous elements (at least 1),
-// sums its squares as a pairwise tree and the wavefront adds the lanes' sums by xor butterflies,
-// which is the balanced tree over the zero-padded row. Bandwidth-bound: 16-byte loads and stores.
+// A wavefront takes R rows, one at a time, after loading all of them; a lane holds C = next_pow2(D) / 64
+// contiguous elements of a row (at least 1), sums its squares as a pairwise tree and the wavefront adds
+// the lanes' sums by xor butterflies, which is the balanced tree over the zero-padded row.
+// Bandwidth-bound: 16-byte loads and stores, R rows of loads in flight a wavefront.
 #include "chess_common.h"
 
 namespace {
 
-constexpr int ROWS_PER_BLOCK = 4;
+constexpr int WAVES = 4;   // wavefronts a workgroup
 
+// naturally aligned vector types of 1 to 16 bytes: a copy of BYTES is one load or store of that width
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <int BYTES> struct Bytes;
 template <> struct Bytes<1> { typedef uint8_t type; };
 template <> struct Bytes<2> { typedef uint16_t type; };
 template <> struct Bytes<4> { typedef uint32_t type; };
-template <> struct Bytes<8> { typedef uint2 type; };
-template <> struct Bytes<16> { typedef uint4 type; };
+template <> struct Bytes<8> { typedef v2u type; };
+template <> struct Bytes<16> { typedef v4u type; };
 
 template <int BYTES> DEVICE void copy_bytes(void* to, const void* from) {
     if constexpr (BYTES <= 16) {
         *reinterpret_cast<typename Bytes<BYTES>::type*>(to) = *reinterpret_cast<const typename Bytes<BYTES>::type*>(from);
     } else {
 #pragma unroll
-        for (int i = 0; i < BYTES / 16; i++) reinterpret_cast<uint4*>(to)[i] = reinterpret_cast<const uint4*>(from)[i];
+        for (int i = 0; i < BYTES / 16; i++) reinterpret_cast<v4u*>(to)[i] = reinterpret_cast<const v4u*>(from)[i];
     }
 }
 
-// C halves from row[col..col+C): one vector load when the row length is a multiple of C, else element by element.
-template <int C> DEVICE void load_halves(const half_t* row, int col, int D, bool vector, float (&out)[C]) {
-    half_t raw[C];
-    if (vector) {
-        if (col < D) {
-            copy_bytes<2 * C>(raw, row + col);
-        } else {
-#pragma unroll
-            for (int i = 0; i < C; i++) raw[i] = (half_t)0.0f;
-        }
+// C halves from row[col..col+C) (the caller zeroes those past D): one vector load when the row length is a multiple
+// of C, from a place clamped into the row, so that no branch holds the load back and the loads of several rows stay in
+// flight together; else element by element.
+template <int C, bool VECTOR> DEVICE void load_raw(const half_t* row, int col, int D, half_t (&raw)[C]) {
+    if constexpr (VECTOR) {
+        copy_bytes<2 * C>(raw, row + min(col, D - C));
     } else {
 #pragma unroll
-        for (int i = 0; i < C; i++) raw[i] = col + i < D ? row[col + i] : (half_t)0.0f;
+        for (int i = 0; i < C; i++) raw[i] = row[min(col + i, D - 1)];
     }
-#pragma unroll
-    for (int i = 0; i < C; i++) out[i] = (float)raw[i];
 }
 
-template <int C>
-__global__ __launch_bounds__(64 * ROWS_PER_BLOCK) void norm_quant_kernel(
+template <int C> DEVICE void widen(const half_t (&raw)[C], int col, int D, float (&out)[C]) {
+#pragma unroll
+    for (int i = 0; i < C; i++) out[i] = col + i < D ? (float)raw[i] : 0.0f;
+}
+
+template <int C, int R, bool VECTOR>
+__global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
     const half_t* __restrict__ x, const half_t* __restrict__ original, const half_t* __restrict__ residual_scale,
     const half_t* __restrict__ input_scale, const half_t* __restrict__ gain, half_t* __restrict__ mixed,
     int8_t* __restrict__ q, float* __restrict__ scale, int M, int D, float eps, int mix)
 {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;  // the whole wavefront leaves together
-    const bool vector = D % C == 0;
+    const int first = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
+    if (first >= M) return;  // the whole wavefront leaves together
+    constexpr bool vector = VECTOR;
     const int col = lane * C;
-    const size_t base = (size_t)row * D;
 
-    float v[C];
-    load_halves<C>(x + base, col, D, vector, v);
+    // the wavefront's R rows (and inputs) are loaded before any is used, so that R rows of loads are in flight
+    half_t raw_x[R][C], raw_o[R][C];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = min(first + r, M - 1);
+        load_raw<C, VECTOR>(x + (size_t)row * D, col, D, raw_x[r]);
+        if (mix) load_raw<C, VECTOR>(original + (size_t)row * D, col, D, raw_o[r]);
+    }
+    half_t raw_g[C];
+    load_raw<C, false>(gain, col, D, raw_g);
+    float g[C];
+    widen<C>(raw_g, col, D, g);
+    float rs = 0.0f, is = 0.0f;
     if (mix) {
-        float o[C];
-        load_halves<C>(original + base, col, D, vector, o);
-        const float rs = (float)residual_scale[0], is = (float)input_scale[0];
-        half_t m[C];
+        rs = (float)residual_scale[0];
+        is = (float)input_scale[0];
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const int row = first + r;
+        if (row >= M) break;
+        const size_t base = (size_t)row * D;
+        float v[C];
+        widen<C>(raw_x[r], col, D, v);
+        if (mix) {
+            float o[C];
+            widen<C>(raw_o[r], col, D, o);
+            half_t m[C];
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                m[i] = (half_t)((v[i] * rs) + (o[i] * is));
+                v[i] = (float)m[i];
+            }
+            if (vector) {
+                if (col < D) copy_bytes<2 * C>(mixed + base + col, m);
+            } else {
+#pragma unroll
+                for (int i = 0; i < C; i++)
+                    if (col + i < D) mixed[base + col + i] = m[i];
+            }
+        }
+
+        // the lane's squares as a pairwise tree, then the wavefront's butterflies
+        float squares[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
+#pragma unroll
+        for (int width = C; width > 1; width >>= 1)
+#pragma unroll
+            for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
+        const float total = wave_sum(squares[0]);
+        const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + eps);
+
+        float y[C];
+        float largest = 0.0f;
 #pragma unroll
         for (int i = 0; i < C; i++) {
-            m[i] = (half_t)((v[i] * rs) + (o[i] * is));
-            v[i] = (float)m[i];
+            y[i] = (v[i] * inverse) * g[i];
+            largest = fmaxf(largest, fabsf(y[i]));
         }
+        const float absmax = fmaxf(wave_max(largest), 1e-20f);
+        const float inverse_step = 127.0f / absmax;
+        int8_t out[C];
+#pragma unroll
+        for (int i = 0; i < C; i++) out[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
         if (vector) {
-            if (col < D) copy_bytes<2 * C>(mixed + base + col, m);
+            if (col < D) copy_bytes<C>(q + base + col, out);
         } else {
 #pragma unroll
             for (int i = 0; i < C; i++)
-                if (col + i < D) mixed[base + col + i] = m[i];
+                if (col + i < D) q[base + col + i] = out[i];
         }
+        if (lane == 0) scale[row] = absmax / 127.0f;
     }
-
-    // the lane's squares as a pairwise tree, then the wavefront's butterflies
-    float squares[C];
-#pragma unroll
-    for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
-#pragma unroll
-    for (int width = C; width > 1; width >>= 1)
-#pragma unroll
-        for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
-    const float total = wave_sum(squares[0]);
-    const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + eps);
-
-    float y[C];
-    float largest = 0.0f;
-#pragma unroll
-    for (int i = 0; i < C; i++) {
-        const float g = col + i < D ? (float)gain[col + i] : 0.0f;
-        y[i] = (v[i] * inverse) * g;
-        largest = fmaxf(largest, fabsf(y[i]));
-    }
-    const float absmax = fmaxf(wave_max(largest), 1e-20f);
-    const float inverse_step = 127.0f / absmax;
-    int8_t out[C];
-#pragma unroll
-    for (int i = 0; i < C; i++) out[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
-    if (vector) {
-        if (col < D) copy_bytes<C>(q + base + col, out);
-    } else {
-#pragma unroll
-        for (int i = 0; i < C; i++)
-            if (col + i < D) q[base + col + i] = out[i];
-    }
-    if (lane == 0) scale[row] = absmax / 127.0f;
 }
 
 template <int C>
 int launch(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
            void* q, void* scale, int M, int D, float eps, hipStream_t stream)
 {
-    const dim3 grid((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK), block(64 * ROWS_PER_BLOCK);
-    hipLaunchKernelGGL(norm_quant_kernel<C>, grid, block, 0, stream, (const half_t*)x, (const half_t*)original,
-                       (const half_t*)residual_scale, (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q,
-                       (float*)scale, M, D, eps, original != nullptr ? 1 : 0);
+    // rows a wavefront: enough loads in flight to stream at HBM speed once the launch fills the chip, one row a
+    // wavefront while it does not
+    constexpr int WIDE = C <= 8 ? 4 : 2;
+    const bool wide = M >= 32768;
+    const int rows_per_block = WAVES * (wide ? WIDE : 1);
+    const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);
+    auto kernel = wide ? (D % C == 0 ? norm_quant_kernel<C, WIDE, true> : norm_quant_kernel<C, WIDE, false>)
+                       : (D % C == 0 ? norm_quant_kernel<C, 1, true> : norm_quant_kernel<C, 1, false>);
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, (const half_t*)x, (const half_t*)original, (const half_t*)residual_scale,
+                       (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q, (float*)scale, M, D, eps,
+                       original != nullptr ? 1 : 0);
     return launch_status();
 }
 

@@ -3,14 +3,14 @@
 // h[M, N] (fp16) is zero-padded to WIDTH columns; each 32-column block is multiplied by Sylvester's
 // H32 as five f32 butterfly stages of spans 1, 2, 4, 8, 16, (a, b) -> (a + b, a - b); then
 // absmax = max(max |r|, 1e-20), q = rint(r * (127 / absmax)), scale = absmax / 127.
-// One wavefront per row. A lane holds 8 consecutive columns (16 bytes) per pass of 512 columns, so
+// A wavefront takes R rows (loaded first, then one at a time). A lane holds 8 consecutive columns (16 bytes) per pass of 512 columns, so
 // four lanes hold a 32-block: spans 1-4 run in the lane, spans 8 and 16 with lanes ^1 and ^2.
 // Bandwidth-bound: 2N bytes in, WIDTH + 4 out per row.
 #include "chess_common.h"
 
 namespace {
 
-constexpr int ROWS_PER_BLOCK = 4;
+constexpr int WAVES = 4;   // wavefronts a workgroup
 constexpr int LANE_COLUMNS = 8;
 constexpr int PASS_COLUMNS = 64 * LANE_COLUMNS;
 
@@ -30,58 +30,76 @@ DEVICE void butterflies(float (&v)[LANE_COLUMNS], int lane) {
         const bool upper = (lane >> bit) & 1;
 #pragma unroll
         for (int i = 0; i < LANE_COLUMNS; i++) {
-            const float other = __shfl_xor(v[i], 1 << bit, 64);
+            const float other = bit == 0 ? lane_xor1(v[i]) : lane_xor2(v[i]);
             v[i] = upper ? other - v[i] : v[i] + other;
         }
     }
 }
 
-template <int PASSES>
-__global__ __launch_bounds__(64 * ROWS_PER_BLOCK) void rotate_quant_kernel(
+template <int PASSES, int R, bool VECTOR>
+__global__ __launch_bounds__(64 * WAVES) void rotate_quant_kernel(
     const half_t* __restrict__ h, int8_t* __restrict__ q, float* __restrict__ scale, int M, int N, int width)
 {
     const int lane = threadIdx.x & 63;
-    const int row = blockIdx.x * ROWS_PER_BLOCK + (threadIdx.x >> 6);
-    if (row >= M) return;
-    const half_t* from = h + (size_t)row * N;
-    const bool vector = N % LANE_COLUMNS == 0;
+    const int first = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
+    if (first >= M) return;
 
-    float v[PASSES][LANE_COLUMNS];
-    float largest = 0.0f;
+    // the wavefront's R rows are loaded before any is used (from places clamped into the rows, zeroed past N after),
+    // so that all their loads are in flight together
+    v8h raw[R][PASSES];
 #pragma unroll
-    for (int pass = 0; pass < PASSES; pass++) {
-        const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
-        half_t raw[LANE_COLUMNS];
-        if (vector && col < N) {
-            *reinterpret_cast<uint4*>(raw) = *reinterpret_cast<const uint4*>(from + col);
-        } else {
+    for (int r = 0; r < R; r++) {
+        const half_t* from = h + (size_t)min(first + r, M - 1) * N;
 #pragma unroll
-            for (int i = 0; i < LANE_COLUMNS; i++) raw[i] = col + i < N ? from[col + i] : (half_t)0.0f;
+        for (int pass = 0; pass < PASSES; pass++) {
+            const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
+            if constexpr (VECTOR) {
+                raw[r][pass] = *reinterpret_cast<const v8h*>(from + min(col, N - LANE_COLUMNS));
+            } else {
+#pragma unroll
+                for (int i = 0; i < LANE_COLUMNS; i++) raw[r][pass][i] = from[min(col + i, N - 1)];
+            }
         }
-#pragma unroll
-        for (int i = 0; i < LANE_COLUMNS; i++) v[pass][i] = (float)raw[i];
-        butterflies(v[pass], lane);
-#pragma unroll
-        for (int i = 0; i < LANE_COLUMNS; i++) largest = fmaxf(largest, fabsf(v[pass][i]));
     }
-    const float absmax = fmaxf(wave_max(largest), 1e-20f);
-    const float inverse_step = 127.0f / absmax;
-    int8_t* to = q + (size_t)row * width;
 #pragma unroll
-    for (int pass = 0; pass < PASSES; pass++) {
-        const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
-        if (col >= width) continue;
-        int8_t out[LANE_COLUMNS];
+    for (int r = 0; r < R; r++) {
+        const int row = first + r;
+        if (row >= M) break;
+        float v[PASSES][LANE_COLUMNS];
+        float largest = 0.0f;
 #pragma unroll
-        for (int i = 0; i < LANE_COLUMNS; i++) out[i] = (int8_t)(int)__builtin_rintf(v[pass][i] * inverse_step);
-        *reinterpret_cast<uint2*>(to + col) = *reinterpret_cast<const uint2*>(out);
+        for (int pass = 0; pass < PASSES; pass++) {
+            const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
+#pragma unroll
+            for (int i = 0; i < LANE_COLUMNS; i++) v[pass][i] = col + i < N ? (float)raw[r][pass][i] : 0.0f;
+            butterflies(v[pass], lane);
+#pragma unroll
+            for (int i = 0; i < LANE_COLUMNS; i++) largest = fmaxf(largest, fabsf(v[pass][i]));
+        }
+        const float absmax = fmaxf(wave_max(largest), 1e-20f);
+        const float inverse_step = 127.0f / absmax;
+        int8_t* to = q + (size_t)row * width;
+#pragma unroll
+        for (int pass = 0; pass < PASSES; pass++) {
+            const int col = pass * PASS_COLUMNS + lane * LANE_COLUMNS;
+            if (col >= width) continue;
+            int8_t out[LANE_COLUMNS];
+#pragma unroll
+            for (int i = 0; i < LANE_COLUMNS; i++) out[i] = (int8_t)(int)__builtin_rintf(v[pass][i] * inverse_step);
+            *reinterpret_cast<uint2*>(to + col) = *reinterpret_cast<const uint2*>(out);
+        }
+        if (lane == 0) scale[row] = absmax / 127.0f;
     }
-    if (lane == 0) scale[row] = absmax / 127.0f;
 }
 
 template <int PASSES> int launch(const void* h, void* q, void* scale, int M, int N, int width, hipStream_t stream) {
-    const dim3 grid((M + ROWS_PER_BLOCK - 1) / ROWS_PER_BLOCK), block(64 * ROWS_PER_BLOCK);
-    hipLaunchKernelGGL(rotate_quant_kernel<PASSES>, grid, block, 0, stream, (const half_t*)h, (int8_t*)q, (float*)scale, M, N, width);
+    constexpr int WIDE = PASSES <= 4 ? 2 : 1;   // rows a wavefront once the launch fills the chip
+    const bool wide = M >= 32768;
+    const int rows_per_block = WAVES * (wide ? WIDE : 1);
+    const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);
+    auto kernel = wide ? (N % LANE_COLUMNS == 0 ? rotate_quant_kernel<PASSES, WIDE, true> : rotate_quant_kernel<PASSES, WIDE, false>)
+                       : (N % LANE_COLUMNS == 0 ? rotate_quant_kernel<PASSES, 1, true> : rotate_quant_kernel<PASSES, 1, false>);
+    hipLaunchKernelGGL(kernel, grid, block, 0, stream, (const half_t*)h, (int8_t*)q, (float*)scale, M, N, width);
     return launch_status();
 }
 
