@@ -73,8 +73,6 @@ template <> struct Mfma<half_t> {
     static DEVICE float value(Acc c, int r) { return c[r]; }
 };
 
-DEVICE v4h quad_halves(const half_t* p) { return *reinterpret_cast<const v4h*>(p); }
-
 // outputs are streamed (non-temporal stores), so that they do not push the operands out of L2
 typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
@@ -121,6 +119,19 @@ template <int OUTSTANDING> DEVICE void stage_barrier() {
     bare_barrier();
 }
 
+// LDS: the ring of stages, reused after the main loop for the staged output tile; then the epilogue's column
+// and row vectors (f32: NB x BN weight scales and BM row scales for int8, BN bias)
+template <typename In, int BM, int BN, int NB, int STAGES, typename OutT, bool PACKED>
+constexpr int vector_offset() {
+    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = PACKED ? BM * (BN + 8) * 2 : BM * (BN + 4) * 4;
+    return RING > STAGING ? RING : STAGING;
+}
+template <typename In, int BM, int BN, int NB, int STAGES, typename OutT, bool PACKED>
+constexpr int lds_bytes() {
+    constexpr bool SCALED = std::is_same<In, int8_t>::value && !std::is_same<OutT, int>::value;
+    return vector_offset<In, BM, BN, NB, STAGES, OutT, PACKED>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
+}
+
 template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
 __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
@@ -165,6 +176,47 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
             source[p] = (const int8_t*)w + ((size_t)group * N + col) * row_bytes + chunk;
         }
     }
+    // The epilogue's operands are loaded now, so that they arrive while the main loop runs instead of after it:
+    // the tile's column vectors (weight scales of the NB row groups, bias) and row scales, parked in LDS after
+    // the loop, and the residual / original rows of phase 2, kept in registers. Past-the-edge places read
+    // the last row / column (never stored).
+    constexpr bool SCALED = INT8 && !RAW;
+    constexpr int VEC_XS = SCALED ? NB * BN : 0, VEC_BIAS = VEC_XS + (SCALED ? BM : 0), VEC = RAW ? 0 : VEC_BIAS + BN;
+    constexpr int VEC_PER_THREAD = (VEC + THREADS - 1) / THREADS;
+    // One unconditional 32-bit load a slot, from a chosen address (a bias half comes in the aligned word that holds
+    // it), kept as raw bits: loads under divergent branches, or converted as they arrive, would be waited for here.
+    uint32_t vec[VEC_PER_THREAD > 0 ? VEC_PER_THREAD : 1];
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++) {
+        const int at = tid + v * THREADS;
+        const uint32_t* from = (const uint32_t*)x;   // any readable word, for slots that hold nothing
+        if (at < VEC_XS) {
+            from = (const uint32_t*)(e.w_scale + (size_t)(at / BN) * N + min(n0 + at % BN, N - 1));
+        } else if (at < VEC_BIAS) {
+            from = (const uint32_t*)(e.x_scale + min(m0 + at - VEC_XS, M - 1));
+        } else if (at < VEC && (e.flags & EPI_BIAS)) {
+            from = (const uint32_t*)e.bias + min(n0 + at - VEC_BIAS, N - 1) / 2;
+        }
+        vec[v] = *from;
+    }
+    uint16_t mix_scales[2] = {0, 0};
+    if (!RAW && (e.flags & EPI_MIX)) {
+        mix_scales[0] = __builtin_bit_cast(uint16_t, e.residual_scale[0]);
+        mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
+    }
+    constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = BM / ROWS;
+    constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
+    const bool vectors = N % 8 == 0;
+    v8h residual_rows[ADDS ? PASSES : 1], original_rows[ADDS ? PASSES : 1];
+    if constexpr (ADDS) {
+#pragma unroll
+        for (int pass = 0; pass < PASSES; pass++) {
+            const size_t at = (size_t)min(m0 + pass * ROWS + tid / ROW_LANES, M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
+            if (vectors && (e.flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
+            if (vectors && (e.flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
+        }
+    }
+
     LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
     auto issue = [&](int step) {
         const int k0 = min(step, steps - 1) * STAGE_K_BYTES;
@@ -215,6 +267,19 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
+    // the prefetched raw bits are first touched here, so that nothing converts (and waits for) them before the loop
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
+    asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
+    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, NB, STAGES, OutT, PACKED>());
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++)
+        if (const int at = tid + v * THREADS; at < VEC) {
+            const int shift = (min(n0 + at - VEC_BIAS, N - 1) & 1) * 16;   // a bias's half of its word
+            vectors_lds[at] = at < VEC_BIAS ? __uint_as_float(vec[v])
+                                            : (e.flags & EPI_BIAS) ? (float)__builtin_bit_cast(half_t, (uint16_t)(vec[v] >> shift)) : 0.0f;
+        }
+    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
     bare_barrier();
 
     // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the tile in LDS: in f32 ([BM][BN + 4])
@@ -222,58 +287,35 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     // A fragment's lane holds row lane % 32 and, in register 4 q + r, column 8 q + 4 (lane / 32) + r.
     float* staged = (float*)lds;
     OutT* packed = (OutT*)lds;
-    const bool quads = N % 4 == 0;
+    const float* column = vectors_lds;   // [NB][BN] weight scales, then [BM] row scales, then [BN] bias
 #pragma unroll
     for (int i = 0; i < FM; i++) {
         const int m_local = wm * WM + i * 32 + in_row;
-        const float xs = (INT8 && !RAW) ? e.x_scale[min(m0 + m_local, M - 1)] : 1.0f;
+        const float xs = SCALED ? column[VEC_XS + m_local] : 1.0f;
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
             for (int q = 0; q < 4; q++) {
                 const int n_local = wn * WN + j * 32 + 8 * q + 4 * half;
-                const int n = n0 + n_local;
                 float value[4];
                 if constexpr (RAW) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) value[r] = __int_as_float((int)acc[0][i][j][4 * q + r]);
                 } else {
-                    float ws[4] = {1.0f, 1.0f, 1.0f, 1.0f}, ws_up[4] = {1.0f, 1.0f, 1.0f, 1.0f}, b[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-                    if (quads && n < N) {
-                        if constexpr (INT8) {
-                            const float4 s4 = *reinterpret_cast<const float4*>(e.w_scale + n);
-                            ws[0] = s4.x; ws[1] = s4.y; ws[2] = s4.z; ws[3] = s4.w;
-                            if constexpr (NB == 2) {
-                                const float4 u4 = *reinterpret_cast<const float4*>(e.w_scale + N + n);
-                                ws_up[0] = u4.x; ws_up[1] = u4.y; ws_up[2] = u4.z; ws_up[3] = u4.w;
-                            }
-                        }
-                        if (e.flags & EPI_BIAS) {
-                            const v4h b4 = quad_halves(e.bias + n);
-#pragma unroll
-                            for (int r = 0; r < 4; r++) b[r] = (float)b4[r];
-                        }
-                    } else {
-#pragma unroll
-                        for (int r = 0; r < 4; r++)
-                            if (n + r < N) {
-                                if constexpr (INT8) {
-                                    ws[r] = e.w_scale[n + r];
-                                    if constexpr (NB == 2) ws_up[r] = e.w_scale[N + n + r];
-                                }
-                                if (e.flags & EPI_BIAS) b[r] = (float)e.bias[n + r];
-                            }
-                    }
+                    const float4 ws = SCALED ? *reinterpret_cast<const float4*>(column + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                    const float4 ws_up = SCALED && NB == 2 ? *reinterpret_cast<const float4*>(column + BN + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                    const float4 b = *reinterpret_cast<const float4*>(column + VEC_BIAS + n_local);
+                    const float ws_r[4] = {ws.x, ws.y, ws.z, ws.w}, ws_up_r[4] = {ws_up.x, ws_up.y, ws_up.z, ws_up.w}, b_r[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
                     for (int r = 0; r < 4; r++) {
                         if constexpr (INT8) {
-                            value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws[r];
+                            value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws_r[r];
                         } else {
                             value[r] = MMA::value(acc[0][i][j], 4 * q + r);
                         }
-                        if (e.flags & EPI_BIAS) value[r] = value[r] + b[r];
+                        if (e.flags & EPI_BIAS) value[r] = value[r] + b_r[r];
                         if constexpr (NB == 2) {
-                            const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up[r] : MMA::value(acc[1][i][j], 4 * q + r);
+                            const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up_r[r] : MMA::value(acc[1][i][j], 4 * q + r);
                             value[r] = silu_fast(value[r]) * up;
                         }
                     }
@@ -293,15 +335,9 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 
     // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
     // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
-    constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES;
-    const bool vectors = N % 8 == 0;
-    float rs = 0.0f, is = 0.0f;
-    if (e.flags & EPI_MIX) {
-        rs = (float)e.residual_scale[0];
-        is = (float)e.input_scale[0];
-    }
+    const float rs = (float)__builtin_bit_cast(half_t, mix_scales[0]), is = (float)__builtin_bit_cast(half_t, mix_scales[1]);
 #pragma unroll
-    for (int pass = 0; pass < BM / ROWS; pass++) {
+    for (int pass = 0; pass < PASSES; pass++) {
         const int m_local = pass * ROWS + tid / ROW_LANES, n_local = (tid % ROW_LANES) * 8;
         const int m = m0 + m_local, n = n0 + n_local;
         if (m >= M || n >= N) continue;
@@ -333,9 +369,8 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         } else {
             if (e.flags & EPI_RESIDUAL) {
                 if (vectors) {
-                    const v8h res = *reinterpret_cast<const v8h*>(e.residual + at);
 #pragma unroll
-                    for (int c = 0; c < 8; c++) value[c] = value[c] + (float)res[c];
+                    for (int c = 0; c < 8; c++) value[c] = value[c] + (float)residual_rows[ADDS ? pass : 0][c];
                 } else {
 #pragma unroll
                     for (int c = 0; c < 8; c++)
@@ -345,9 +380,8 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
             if (e.flags & EPI_MIX) {
                 float original[8];
                 if (vectors) {
-                    const v8h o = *reinterpret_cast<const v8h*>(e.original + at);
 #pragma unroll
-                    for (int c = 0; c < 8; c++) original[c] = (float)o[c];
+                    for (int c = 0; c < 8; c++) original[c] = (float)original_rows[ADDS ? pass : 0][c];
                 } else {
 #pragma unroll
                     for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
@@ -368,8 +402,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 
 template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
 int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
-    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = PACKED ? BM * (BN + 8) * 2 : BM * (BN + 4) * 4;
-    constexpr int BYTES = RING > STAGING ? RING : STAGING;
+    constexpr int BYTES = lds_bytes<In, BM, BN, NB, STAGES, OutT, PACKED>();
     auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED>;
     if (BYTES > 65536) {
         static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
