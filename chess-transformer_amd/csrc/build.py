@@ -22,7 +22,9 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off and IEEE divide/sqrt: the f32 op order the kernels declare is what runs.
 # -packed-fp32-ops off: hipcc would otherwise pair f32 ops into v_pk_* instructions by itself.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
-         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
+         "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function",
+         # MFMA results in ordinary VGPRs: no accumulator-register copies before the epilogue reads them
+         "-mllvm", "-amdgpu-mfma-vgpr-form"]
 
 
 def compile_one(source: str) -> Path:

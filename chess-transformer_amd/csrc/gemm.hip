@@ -132,7 +132,7 @@ constexpr int lds_bytes() {
     return vector_offset<In, BM, BN, NB, STAGES, OutT, PACKED>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
 __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
 {
@@ -147,8 +147,12 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     static_assert(BLOCKS % 4 == 0 && FM >= 1 && FN >= 1, "tile shape");
     extern __shared__ __align__(16) int8_t lds[];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // the wavefront as a scalar (the compiler takes tid / 64 for a per-lane value): block indices, LDS destinations
+    // and the branches on them stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    // the epilogue's flags: fixed by the instantiation (EPI >= 0, the network's combinations), else read at run time
+    const int flags = EPI >= 0 ? EPI : e.flags;
     const size_t row_bytes = (size_t)K * sizeof(In);
     const int steps = (int)(row_bytes / STAGE_K_BYTES);
 
@@ -163,17 +167,19 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 
     // this lane's source in each of the wavefront's blocks: row lane / 4 of the block, 16-byte chunk (lane % 4) ^ (lane / 16).
     // Rows past M read row M - 1 and columns past N read column N - 1: their sums are never stored.
-    const int8_t* source[PER_WAVE];
+    // A block's source is a scalar base (x or w, the block index being the same in all lanes) plus a 32-bit lane
+    // offset, so that the step's loads take the scalar-base form with no per-step address arithmetic in the lanes.
+    uint32_t source[PER_WAVE];
 #pragma unroll
     for (int p = 0; p < PER_WAVE; p++) {
         const int block = wave * PER_WAVE + p;
         const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * 16 + (lane >> 2);
         const int chunk = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
         if (block < A_BLOCKS) {
-            source[p] = (const int8_t*)x + (size_t)min(m0 + row, M - 1) * row_bytes + chunk;
+            source[p] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)row_bytes + chunk;
         } else {
             const int group = row / BN, col = min(n0 + row % BN, N - 1);
-            source[p] = (const int8_t*)w + ((size_t)group * N + col) * row_bytes + chunk;
+            source[p] = (uint32_t)(group * N + col) * (uint32_t)row_bytes + chunk;
         }
     }
     // The epilogue's operands are loaded now, so that they arrive while the main loop runs instead of after it:
@@ -194,13 +200,13 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
             from = (const uint32_t*)(e.w_scale + (size_t)(at / BN) * N + min(n0 + at % BN, N - 1));
         } else if (at < VEC_BIAS) {
             from = (const uint32_t*)(e.x_scale + min(m0 + at - VEC_XS, M - 1));
-        } else if (at < VEC && (e.flags & EPI_BIAS)) {
+        } else if (at < VEC && (flags & EPI_BIAS)) {
             from = (const uint32_t*)e.bias + min(n0 + at - VEC_BIAS, N - 1) / 2;
         }
         vec[v] = *from;
     }
     uint16_t mix_scales[2] = {0, 0};
-    if (!RAW && (e.flags & EPI_MIX)) {
+    if (!RAW && (flags & EPI_MIX)) {
         mix_scales[0] = __builtin_bit_cast(uint16_t, e.residual_scale[0]);
         mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
     }
@@ -212,8 +218,8 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
         for (int pass = 0; pass < PASSES; pass++) {
             const size_t at = (size_t)min(m0 + pass * ROWS + tid / ROW_LANES, M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
-            if (vectors && (e.flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
-            if (vectors && (e.flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
+            if (vectors && (flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
+            if (vectors && (flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
         }
     }
 
@@ -222,19 +228,13 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         const int k0 = min(step, steps - 1) * STAGE_K_BYTES;
         LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
 #pragma unroll
-        for (int p = 0; p < PER_WAVE; p++)
-            __builtin_amdgcn_global_load_lds((const void*)(source[p] + k0), (LDS_SPACE void*)(stage + (wave * PER_WAVE + p) * BLOCK), 16, 0, 0);
+        for (int p = 0; p < PER_WAVE; p++) {
+            const int8_t* base = (wave * PER_WAVE + p < A_BLOCKS ? (const int8_t*)x : (const int8_t*)w) + k0;
+            __builtin_amdgcn_global_load_lds((const void*)(base + source[p]), (LDS_SPACE void*)(stage + (wave * PER_WAVE + p) * BLOCK), 16, 0, 0);
+        }
     };
 
     typename MMA::Acc acc[NB][FM][FN];
-#pragma unroll
-    for (int g = 0; g < NB; g++)
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) acc[g][i][j][r] = 0;
 
     // an operand lane (row lane % 32, 16-byte half lane / 32 of each 32-byte sub-step) in a stage: the block of its
     // 16 rows, then the slot 4 r + (chunk ^ (r / 4)) of row r's chunk
@@ -245,10 +245,9 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 
 #pragma unroll
     for (int s = 0; s < STAGES - 1; s++) issue(s);
-    for (int step = 0; step < steps; step++) {
-        stage_barrier<PER_WAVE * (STAGES - 2)>();
-        issue(step + STAGES - 1);   // into the stage read one step ago; past the end it loads the last step again
-        const LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
+    // a step's MFMAs; the first step's start from zero sums (the MFMA's zero accumulator operand), so nothing clears them
+    auto multiply = [&](const LDS_SPACE int8_t* stage, auto first_step) {
+        constexpr bool FIRST = decltype(first_step)::value;
 #pragma unroll
         for (int sub = 0; sub < 2; sub++) {
             typename MMA::Operand af[FM];
@@ -262,8 +261,19 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                     const typename MMA::Operand bf =
                         *(const LDS_SPACE typename MMA::Operand*)(stage + (A_BLOCKS + (g * BN + wn * WN + j * 32) / 16) * BLOCK + operand[sub]);
 #pragma unroll
-                    for (int i = 0; i < FM; i++) acc[g][i][j] = MMA::step(bf, af[i], acc[g][i][j]);
+                    for (int i = 0; i < FM; i++)
+                        acc[g][i][j] = MMA::step(bf, af[i], FIRST && sub == 0 ? typename MMA::Acc{} : acc[g][i][j]);
                 }
+        }
+    };
+    for (int step = 0; step < steps; step++) {
+        stage_barrier<PER_WAVE * (STAGES - 2)>();
+        issue(step + STAGES - 1);   // into the stage read one step ago; past the end it loads the last step again
+        const LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
+        if (step == 0) {
+            multiply(stage, std::true_type{});
+        } else {
+            multiply(stage, std::false_type{});
         }
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
@@ -277,7 +287,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         if (const int at = tid + v * THREADS; at < VEC) {
             const int shift = (min(n0 + at - VEC_BIAS, N - 1) & 1) * 16;   // a bias's half of its word
             vectors_lds[at] = at < VEC_BIAS ? __uint_as_float(vec[v])
-                                            : (e.flags & EPI_BIAS) ? (float)__builtin_bit_cast(half_t, (uint16_t)(vec[v] >> shift)) : 0.0f;
+                                            : (flags & EPI_BIAS) ? (float)__builtin_bit_cast(half_t, (uint16_t)(vec[v] >> shift)) : 0.0f;
         }
     __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
     bare_barrier();
@@ -313,7 +323,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                         } else {
                             value[r] = MMA::value(acc[0][i][j], 4 * q + r);
                         }
-                        if (e.flags & EPI_BIAS) value[r] = value[r] + b_r[r];
+                        if (flags & EPI_BIAS) value[r] = value[r] + b_r[r];
                         if constexpr (NB == 2) {
                             const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up_r[r] : MMA::value(acc[1][i][j], 4 * q + r);
                             value[r] = silu_fast(value[r]) * up;
@@ -367,7 +377,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                     if (n + c < N) out[at + c] = __float_as_int(value[c]);
             }
         } else {
-            if (e.flags & EPI_RESIDUAL) {
+            if (flags & EPI_RESIDUAL) {
                 if (vectors) {
 #pragma unroll
                     for (int c = 0; c < 8; c++) value[c] = value[c] + (float)residual_rows[ADDS ? pass : 0][c];
@@ -377,7 +387,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                         if (n + c < N) value[c] = value[c] + (float)e.residual[at + c];
                 }
             }
-            if (e.flags & EPI_MIX) {
+            if (flags & EPI_MIX) {
                 float original[8];
                 if (vectors) {
 #pragma unroll
@@ -400,10 +410,10 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     }
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
 int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
     constexpr int BYTES = lds_bytes<In, BM, BN, NB, STAGES, OutT, PACKED>();
-    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED>;
+    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED, EPI>;
     if (BYTES > 65536) {
         static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
         if (allowed != hipSuccess) return (int)allowed;
@@ -419,18 +429,18 @@ constexpr int TILES = 9;
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
 // 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3). 0 picks by the launch's size.
-template <typename In, int NB, typename OutT, bool PACKED>
+template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
-        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 6: return launch<In, 256, 64, 4, 1, NB, 4, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
-        default: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED>(x, w, out, e, M, N, K, stream);
+        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 6: return launch<In, 256, 64, 4, 1, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        default: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
     }
 }
 
@@ -441,16 +451,27 @@ int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, 
         const long large = (long)((M + 255) / 256) * ((N + 127) / 128);
         tile = large >= 512 ? 4 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
     }
-    if constexpr (sizeof(OutT) == 2) {
-        if (!(e.flags & (EPI_RESIDUAL | EPI_MIX))) return by_tile<In, NB, OutT, true>(x, w, out, e, M, N, K, tile, stream);
+    // the network's epilogues are built with their flags fixed; any other combination reads them at run time
+    const int f = e.flags;
+    if constexpr (std::is_same<OutT, half_t>::value) {
+        if (NB == 2 && f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);
+        if (NB == 1 && f == EPI_BIAS) return by_tile<In, NB, OutT, true, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);
+        if (NB == 1 && f == EPI_RESIDUAL) return by_tile<In, NB, OutT, false, EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+        if (NB == 1 && f == (EPI_RESIDUAL | EPI_MIX)) return by_tile<In, NB, OutT, false, EPI_RESIDUAL | EPI_MIX>(x, w, out, e, M, N, K, tile, stream);
+        if (NB == 1 && f == (EPI_BIAS | EPI_RESIDUAL)) return by_tile<In, NB, OutT, false, EPI_BIAS | EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
     }
-    return by_tile<In, NB, OutT, false>(x, w, out, e, M, N, K, tile, stream);
+    if constexpr (sizeof(OutT) == 2) {
+        if (!(f & (EPI_RESIDUAL | EPI_MIX))) return by_tile<In, NB, OutT, true, -1>(x, w, out, e, M, N, K, tile, stream);
+    }
+    return by_tile<In, NB, OutT, false, -1>(x, w, out, e, M, N, K, tile, stream);
 }
 
 int check(const void* x, const void* w, void* out, int M, int N, int K, int depth, int tile, const char* what) {
     if (M < 0 || N <= 0 || K <= 0) return chess_fail(CHESS_INVALID_SHAPE, "%s: M %d, N %d, K %d", what, M, N, K);
     if (K % depth != 0) return chess_fail(CHESS_INVALID_SHAPE, "%s reads the %d inputs %d at a time", what, K, depth);
     if (!x || !w || !out) return chess_fail(CHESS_INVALID_SHAPE, "%s: a required pointer is null", what);
+    if ((uint64_t)M * K * (depth == STAGE_K_BYTES ? 1 : 2) >= (1ull << 32) || (uint64_t)2 * N * K * (depth == STAGE_K_BYTES ? 1 : 2) >= (1ull << 32))
+        return chess_fail(CHESS_UNSUPPORTED, "%s addresses its operands with 32-bit offsets: %d x %d and %d x %d are too large", what, M, K, N, K);
     if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return chess_fail(CHESS_MISALIGNED, "%s's 16-byte loads need aligned x, w and out", what);
     if (tile < 0 || tile > TILES) return chess_fail(CHESS_UNSUPPORTED, "tile %d is none of 0 (by size) to %d", tile, TILES);
     return CHESS_OK;

@@ -27,7 +27,7 @@ INT8_DEPTH = 64
 # MI355X: 1 is 64 x 64, 2 128 x 128, 3 128 x 64, 4 256 x 128, 5 128 x 256, 6 256 x 64 (rows x outputs, a 4-stage ring),
 # 7 128 x 128, 8 128 x 64, 9 256 x 64 (a 3-stage ring, more workgroups a compute unit). Every tile gives the same bits.
 INT8_TILES = {"gfx950": {"projection": [(4, 1), (math.inf, 7)],
-                         "gate_up": [(4, 1), (math.inf, 8)],
+                         "gate_up": [(4, 1), (math.inf, 9)],
                          "down": [(32, 1), (math.inf, 7)]}}
 # rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit
 NORM_ROWS = 4
