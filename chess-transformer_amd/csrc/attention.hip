@@ -33,6 +33,19 @@ DEVICE float dot2(uint32_t a, uint32_t b, float c) {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, a), __builtin_bit_cast(h2, b), c, false);
 }
 
+// A 16-byte LDS read of DMA'd data as an instruction of its own, waited for by lgkmcnt and passed through an empty
+// asm so that no use moves above the wait: read through a pointer, the compiler would first wait for every DMA in
+// flight (the next group's rows too), unable to tell the addresses apart.
+DEVICE uint4 lds_read16_settled(const LDS_SPACE void* p) {
+    v4u v;
+    asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"((uint32_t)(uintptr_t)p) : "memory");
+    return uint4{v[0], v[1], v[2], v[3]};
+}
+
+DEVICE void lds_write8(LDS_SPACE void* p, uint2 v) {
+    asm volatile("ds_write_b64 %0, %1" : : "v"((uint32_t)(uintptr_t)p), "v"(v) : "memory");
+}
+
 // the sum of squares of 8 halves
 DEVICE float squares8(const v8h& v, float c) {
     const uint4 w = __builtin_bit_cast(uint4, v);
@@ -55,8 +68,9 @@ struct Layout {
     static constexpr int RAW_K_BYTES = KEYS * DQP * 2;
     static constexpr int RAW_V_BYTES = VKEYS * DV * 2;
     static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
+    static constexpr int COEF_BYTES = 64 * MAX_TEMPLATES * 2;   // a head's template coefficients, a square query a row
     static constexpr int FIXED_BYTES = KEYS_BYTES + VALUES_BYTES + RAW_K_BYTES + RAW_V_BYTES;
-    static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * RAW_Q_BYTES; }
+    static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * (RAW_Q_BYTES + COEF_BYTES); }
 };
 
 // Raw rows are DMA'd 64 16-byte chunks an instruction, the chunks of a row in a swizzled order: chunk c of row r
@@ -100,6 +114,7 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
     LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)(lds + L::KEYS_BYTES + L::VALUES_BYTES);
     LDS_SPACE int8_t* raw_v = raw_k + L::RAW_K_BYTES;
     LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES;     // [2][per_kv][KEYS * DQP halves]
+    LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int lane = threadIdx.x & 63, slab = threadIdx.x >> 6;
     const int threads = blockDim.x, waves = threads / 64;
@@ -127,6 +142,11 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
             for (int hi = 0; hi < per_kv; hi++)
                 dma_rows<KC>(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, tiles * 16, T - 1, width,
                              slab, waves, lane);
+            if (templates_count == MAX_TEMPLATES) {
+                for (int hi = slab; hi < per_kv; hi += waves)
+                    __builtin_amdgcn_global_load_lds((const void*)(board + (size_t)lane * width + c_offset + (group * per_kv + hi) * MAX_TEMPLATES),
+                                                     (LDS_SPACE void*)(raw_c + (buffer * per_kv + hi) * L::COEF_BYTES), 16, 0, 0);
+            }
         }
     };
     dma_group(blockIdx.x * groups_per_block, true, true, 0);
@@ -165,6 +185,24 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
         k_gains[e] = d < dq ? gain : (half_t)0.0f;
     }
     const float inverse_dq = 1.0f / (float)dq;
+    // The templates and gains have landed before the loop (with the first group's rows): counting loads across the
+    // loop's iterations, the compiler would otherwise wait for every load in flight -- the next group's rows too --
+    // at each use of them in the loop.
+    __builtin_amdgcn_s_waitcnt(0);
+
+    // A group's outputs are staged in its query buffer, each wavefront writing its own query rows of each head over
+    // the queries it has read (the value width is at most the query width), and written out when the next group
+    // starts -- 16 bytes a lane along the rows, where the wait at the start of the group after finds them long done.
+    // Stored straight from the MFMA layout, 8 bytes a lane scattered over 16 rows, they would be waited for at once.
+    constexpr bool STAGED = DV <= DQP;
+    auto write_out = [&](int group, int buffer) {
+        constexpr int CHUNKS = DV / 8;
+        for (int item = threadIdx.x; item < per_kv * T * CHUNKS; item += threads) {
+            const int hi = item / (T * CHUNKS), rest = item % (T * CHUNKS), q = rest / CHUNKS, c = rest % CHUNKS;
+            const uint4 eight = lds_read16_settled(raw_q + (buffer * per_kv + hi) * head_bytes + raw_slot<KC>(q, c) * 16);
+            *reinterpret_cast<uint4*>(out + ((size_t)b * T + q) * (heads * DV) + (group * per_kv + hi) * DV + c * 8) = eight;
+        }
+    };
 
     for (int gi = 0; gi < groups_per_block; gi++) {
         const int group = blockIdx.x * groups_per_block + gi;
@@ -172,6 +210,8 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
         // this group's raw rows have landed (this wavefront's DMA), and every wavefront is past the previous group
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        // the previous group's outputs leave its query buffer before the next group's queries come into it
+        if (STAGED && gi > 0) write_out(group - 1, buffer ^ 1);
         if (gi + 1 < groups_per_block) dma_group(group + 1, false, true, buffer ^ 1);
 
         // keys, normalised with the gain: a thread a 16-byte chunk, KC adjacent lanes a key
@@ -213,7 +253,7 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
             {
                 const half_t* from = board + (size_t)min(query, 63) * width + c_offset + head * templates_count;
                 if (templates_count == MAX_TEMPLATES) {
-                    coefficients = *reinterpret_cast<const uint4*>(from);
+                    coefficients = lds_read16_settled(raw_c + (buffer * per_kv + hi) * L::COEF_BYTES + min(query, 63) * 16);
                 } else {
                     uint16_t c[MAX_TEMPLATES];
 #pragma unroll
@@ -315,7 +355,16 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
                     o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
                 }
             }
-            if (query_ok) {
+            if constexpr (STAGED) {
+                // over this query's own row of the head's queries: columns 16 dt + 4 quad .. + 4 are chunk 2 dt + quad / 2
+                LDS_SPACE int8_t* row = raw_q + (buffer * per_kv + hi) * head_bytes;
+#pragma unroll
+                for (int dt = 0; dt < DV / 16; dt++) {
+                    const v4h result = v4h{(half_t)(o[dt][0] * inverse_total), (half_t)(o[dt][1] * inverse_total),
+                                           (half_t)(o[dt][2] * inverse_total), (half_t)(o[dt][3] * inverse_total)};
+                    lds_write8(row + raw_slot<KC>(query, 2 * dt + quad / 2) * 16 + (quad & 1) * 8, __builtin_bit_cast(uint2, result));
+                }
+            } else if (query_ok) {
                 half_t* to = out + ((size_t)b * T + query) * (heads * DV) + head * DV + quad * 4;
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
@@ -325,6 +374,11 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
                 }
             }
         }
+    }
+    if constexpr (STAGED) {
+        __builtin_amdgcn_s_waitcnt(0);   // this wavefront's staging writes are done (the compiler does not see them)
+        __syncthreads();
+        write_out(blockIdx.x * groups_per_block + groups_per_block - 1, (groups_per_block - 1) & 1);
     }
 }
 
