@@ -119,17 +119,22 @@ template <int OUTSTANDING> DEVICE void stage_barrier() {
     bare_barrier();
 }
 
+// An f32 staged tile (an epilogue that still adds to it) is staged half its rows at a time when every wavefront
+// has two or more row fragments: half the LDS, so that more workgroups fit a CU.
+template <int BM, int WAVES_M, bool PACKED> constexpr int staging_halves() { return !PACKED && (BM / WAVES_M / 32) % 2 == 0 ? 2 : 1; }
+
 // LDS: the ring of stages, reused after the main loop for the staged output tile; then the epilogue's column
 // and row vectors (f32: NB x BN weight scales and BM row scales for int8, BN bias)
-template <typename In, int BM, int BN, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED>
 constexpr int vector_offset() {
-    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK, STAGING = PACKED ? BM * (BN + 8) * 2 : BM * (BN + 4) * 4;
+    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK;
+    constexpr int STAGING = PACKED ? BM * (BN + 8) * 2 : BM / staging_halves<BM, WAVES_M, PACKED>() * (BN + 4) * 4;
     return RING > STAGING ? RING : STAGING;
 }
-template <typename In, int BM, int BN, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED>
 constexpr int lds_bytes() {
     constexpr bool SCALED = std::is_same<In, int8_t>::value && !std::is_same<OutT, int>::value;
-    return vector_offset<In, BM, BN, NB, STAGES, OutT, PACKED>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
+    return vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
 }
 
 template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
@@ -211,13 +216,22 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
     }
     constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = BM / ROWS;
+    // Staged in halves, half h holds row fragments h * HALF_FM .. of every wavefront: staged row r is tile row
+    // (r / HALF_ROWS) * WM + h * HALF_ROWS + r % HALF_ROWS.
+    constexpr int HALVES = staging_halves<BM, WAVES_M, PACKED>(), HALF_FM = FM / HALVES, HALF_ROWS = WM / HALVES;
+    constexpr int HALF_PASSES = PASSES / HALVES;
+    static_assert(PASSES % HALVES == 0, "passes split between the halves");
+    auto pass_row = [&](int pass) {   // the tile row a lane takes in phase 2's pass
+        const int staged_row = pass % HALF_PASSES * ROWS + tid / ROW_LANES;
+        return HALVES == 1 ? staged_row : staged_row / HALF_ROWS * WM + pass / HALF_PASSES * HALF_ROWS + staged_row % HALF_ROWS;
+    };
     constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
     const bool vectors = N % 8 == 0;
     v8h residual_rows[ADDS ? PASSES : 1], original_rows[ADDS ? PASSES : 1];
     if constexpr (ADDS) {
 #pragma unroll
         for (int pass = 0; pass < PASSES; pass++) {
-            const size_t at = (size_t)min(m0 + pass * ROWS + tid / ROW_LANES, M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
+            const size_t at = (size_t)min(m0 + pass_row(pass), M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
             if (vectors && (flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
             if (vectors && (flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
         }
@@ -281,7 +295,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
     asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
-    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, NB, STAGES, OutT, PACKED>());
+    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>());
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++)
         if (const int at = tid + v * THREADS; at < VEC) {
@@ -292,119 +306,131 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
     bare_barrier();
 
-    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the tile in LDS: in f32 ([BM][BN + 4])
-    // when phase 2 still adds to it, else (PACKED) already rounded to the 16-bit output ([BM][BN + 8]).
+    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the tile in LDS: in f32 ([BM][BN + 4], or
+    // half the rows at a time, each half then taken by phase 2) when phase 2 still adds to it, else (PACKED) already
+    // rounded to the 16-bit output ([BM][BN + 8]).
     // A fragment's lane holds row lane % 32 and, in register 4 q + r, column 8 q + 4 (lane / 32) + r.
     float* staged = (float*)lds;
     OutT* packed = (OutT*)lds;
     const float* column = vectors_lds;   // [NB][BN] weight scales, then [BM] row scales, then [BN] bias
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-        const int m_local = wm * WM + i * 32 + in_row;
-        const float xs = SCALED ? column[VEC_XS + m_local] : 1.0f;
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const int n_local = wn * WN + j * 32 + 8 * q + 4 * half;
-                float value[4];
-                if constexpr (RAW) {
-#pragma unroll
-                    for (int r = 0; r < 4; r++) value[r] = __int_as_float((int)acc[0][i][j][4 * q + r]);
-                } else {
-                    const float4 ws = SCALED ? *reinterpret_cast<const float4*>(column + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
-                    const float4 ws_up = SCALED && NB == 2 ? *reinterpret_cast<const float4*>(column + BN + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
-                    const float4 b = *reinterpret_cast<const float4*>(column + VEC_BIAS + n_local);
-                    const float ws_r[4] = {ws.x, ws.y, ws.z, ws.w}, ws_up_r[4] = {ws_up.x, ws_up.y, ws_up.z, ws_up.w}, b_r[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        if constexpr (INT8) {
-                            value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws_r[r];
-                        } else {
-                            value[r] = MMA::value(acc[0][i][j], 4 * q + r);
-                        }
-                        if (flags & EPI_BIAS) value[r] = value[r] + b_r[r];
-                        if constexpr (NB == 2) {
-                            const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up_r[r] : MMA::value(acc[1][i][j], 4 * q + r);
-                            value[r] = silu_fast(value[r]) * up;
-                        }
-                    }
-                }
-                if constexpr (PACKED) {
-                    // the f32 value is what rounds: keep its last multiply out of the conversion (one rounding, not two)
-#pragma unroll
-                    for (int r = 0; r < 4; r++) asm volatile("" : "+v"(value[r]));
-                    stage_four<OutT>(packed + m_local * (BN + 8) + n_local, value);
-                } else {
-                    *reinterpret_cast<float4*>(staged + m_local * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
-                }
-            }
-    }
-    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
-    bare_barrier();
-
-    // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
-    // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
     const float rs = (float)__builtin_bit_cast(half_t, mix_scales[0]), is = (float)__builtin_bit_cast(half_t, mix_scales[1]);
 #pragma unroll
-    for (int pass = 0; pass < PASSES; pass++) {
-        const int m_local = pass * ROWS + tid / ROW_LANES, n_local = (tid % ROW_LANES) * 8;
-        const int m = m0 + m_local, n = n0 + n_local;
-        if (m >= M || n >= N) continue;
-        const size_t at = (size_t)m * N + n;
-        if constexpr (PACKED) {
-            const uint4 eight = *reinterpret_cast<const uint4*>(packed + m_local * (BN + 8) + n_local);
-            if (vectors) {
-                __builtin_nontemporal_store(__builtin_bit_cast(v4u, eight), reinterpret_cast<v4u*>(out + at));
-            } else {
-                const OutT* values = reinterpret_cast<const OutT*>(&eight);
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-                    if (n + c < N) out[at + c] = values[c];
-            }
-            continue;
+    for (int h = 0; h < HALVES; h++) {
+        if (h > 0) {
+            __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // the previous half's staged rows are read
+            bare_barrier();
         }
-        const float4 lo = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local);
-        const float4 hi = *reinterpret_cast<const float4*>(staged + m_local * (BN + 4) + n_local + 4);
-        float value[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
-        if constexpr (RAW) {
-            if (vectors) {
-                *reinterpret_cast<uint4*>(out + at) = uint4{__float_as_uint(value[0]), __float_as_uint(value[1]), __float_as_uint(value[2]), __float_as_uint(value[3])};
-                *reinterpret_cast<uint4*>(out + at + 4) = uint4{__float_as_uint(value[4]), __float_as_uint(value[5]), __float_as_uint(value[6]), __float_as_uint(value[7])};
-            } else {
 #pragma unroll
-                for (int c = 0; c < 8; c++)
-                    if (n + c < N) out[at + c] = __float_as_int(value[c]);
-            }
-        } else {
-            if (flags & EPI_RESIDUAL) {
+        for (int fi = 0; fi < HALF_FM; fi++) {
+            const int i = h * HALF_FM + fi;
+            const int m_local = wm * WM + i * 32 + in_row;
+            const int staged_row = HALVES == 1 ? m_local : wm * HALF_ROWS + fi * 32 + in_row;
+            const float xs = SCALED ? column[VEC_XS + m_local] : 1.0f;
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n_local = wn * WN + j * 32 + 8 * q + 4 * half;
+                    float value[4];
+                    if constexpr (RAW) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) value[r] = __int_as_float((int)acc[0][i][j][4 * q + r]);
+                    } else {
+                        const float4 ws = SCALED ? *reinterpret_cast<const float4*>(column + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                        const float4 ws_up = SCALED && NB == 2 ? *reinterpret_cast<const float4*>(column + BN + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                        const float4 b = *reinterpret_cast<const float4*>(column + VEC_BIAS + n_local);
+                        const float ws_r[4] = {ws.x, ws.y, ws.z, ws.w}, ws_up_r[4] = {ws_up.x, ws_up.y, ws_up.z, ws_up.w}, b_r[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            if constexpr (INT8) {
+                                value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws_r[r];
+                            } else {
+                                value[r] = MMA::value(acc[0][i][j], 4 * q + r);
+                            }
+                            if (flags & EPI_BIAS) value[r] = value[r] + b_r[r];
+                            if constexpr (NB == 2) {
+                                const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up_r[r] : MMA::value(acc[1][i][j], 4 * q + r);
+                                value[r] = silu_fast(value[r]) * up;
+                            }
+                        }
+                    }
+                    if constexpr (PACKED) {
+                        // the f32 value is what rounds: keep its last multiply out of the conversion (one rounding, not two)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) asm volatile("" : "+v"(value[r]));
+                        stage_four<OutT>(packed + m_local * (BN + 8) + n_local, value);
+                    } else {
+                        *reinterpret_cast<float4*>(staged + staged_row * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
+                    }
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
+        bare_barrier();
+
+        // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
+        // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
+#pragma unroll
+        for (int hp = 0; hp < HALF_PASSES; hp++) {
+            const int pass = h * HALF_PASSES + hp;
+            const int staged_row = hp * ROWS + tid / ROW_LANES;
+            const int m_local = pass_row(pass), n_local = (tid % ROW_LANES) * 8;
+            const int m = m0 + m_local, n = n0 + n_local;
+            if (m >= M || n >= N) continue;
+            const size_t at = (size_t)m * N + n;
+            if constexpr (PACKED) {
+                const uint4 eight = *reinterpret_cast<const uint4*>(packed + staged_row * (BN + 8) + n_local);
                 if (vectors) {
+                    __builtin_nontemporal_store(__builtin_bit_cast(v4u, eight), reinterpret_cast<v4u*>(out + at));
+                } else {
+                    const OutT* values = reinterpret_cast<const OutT*>(&eight);
 #pragma unroll
-                    for (int c = 0; c < 8; c++) value[c] = value[c] + (float)residual_rows[ADDS ? pass : 0][c];
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) out[at + c] = values[c];
+                }
+                continue;
+            }
+            const float4 lo = *reinterpret_cast<const float4*>(staged + staged_row * (BN + 4) + n_local);
+            const float4 hi = *reinterpret_cast<const float4*>(staged + staged_row * (BN + 4) + n_local + 4);
+            float value[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            if constexpr (RAW) {
+                if (vectors) {
+                    *reinterpret_cast<uint4*>(out + at) = uint4{__float_as_uint(value[0]), __float_as_uint(value[1]), __float_as_uint(value[2]), __float_as_uint(value[3])};
+                    *reinterpret_cast<uint4*>(out + at + 4) = uint4{__float_as_uint(value[4]), __float_as_uint(value[5]), __float_as_uint(value[6]), __float_as_uint(value[7])};
                 } else {
 #pragma unroll
                     for (int c = 0; c < 8; c++)
-                        if (n + c < N) value[c] = value[c] + (float)e.residual[at + c];
+                        if (n + c < N) out[at + c] = __float_as_int(value[c]);
                 }
-            }
-            if (flags & EPI_MIX) {
-                float original[8];
-                if (vectors) {
+            } else {
+                if (flags & EPI_RESIDUAL) {
+                    if (vectors) {
 #pragma unroll
-                    for (int c = 0; c < 8; c++) original[c] = (float)original_rows[ADDS ? pass : 0][c];
+                        for (int c = 0; c < 8; c++) value[c] = value[c] + (float)residual_rows[ADDS ? pass : 0][c];
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; c++)
+                            if (n + c < N) value[c] = value[c] + (float)e.residual[at + c];
+                    }
+                }
+                if (flags & EPI_MIX) {
+                    float original[8];
+                    if (vectors) {
+#pragma unroll
+                        for (int c = 0; c < 8; c++) original[c] = (float)original_rows[ADDS ? pass : 0][c];
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
+                    }
+#pragma unroll
+                    for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
+                }
+                if (vectors) {
+                    store_eight<OutT>(out + at, value);
                 } else {
 #pragma unroll
-                    for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) out[at + c] = from_float<OutT>(value[c]);
                 }
-#pragma unroll
-                for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
-            }
-            if (vectors) {
-                store_eight<OutT>(out + at, value);
-            } else {
-#pragma unroll
-                for (int c = 0; c < 8; c++)
-                    if (n + c < N) out[at + c] = from_float<OutT>(value[c]);
             }
         }
     }
@@ -412,7 +438,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 
 template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
 int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
-    constexpr int BYTES = lds_bytes<In, BM, BN, NB, STAGES, OutT, PACKED>();
+    constexpr int BYTES = lds_bytes<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>();
     auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED, EPI>;
     if (BYTES > 65536) {
         static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
@@ -423,12 +449,13 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
     return launch_status();
 }
 
-constexpr int TILES = 9;
+constexpr int TILES = 11;
 
 // The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
-// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3). 0 picks by the launch's size.
+// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
+// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2). 0 picks by the launch's size.
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
@@ -440,7 +467,9 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
         case 6: return launch<In, 256, 64, 4, 1, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
-        default: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 9: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 10: return launch<In, 256, 64, 4, 1, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        default: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
     }
 }
 

@@ -23,7 +23,7 @@ from model.model import EDGE, KING, KNIGHT, NO_PIECE, PAWN, QUEEN, THEIRS, Chess
 LINEAR_DEPTH, GROUP_M = 32, 8
 FEATURE_SLOTS = 23
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
-LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
+LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 11)]}
 # positions a launch should reach before a workgroup takes several key/value groups
 ATTENTION_WORKGROUPS = 1024
 

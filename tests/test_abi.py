@@ -57,10 +57,10 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_rotate_quant(16, 16, 16, 4, 100, 100, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 100, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert b"64 at a time" in library.chess_last_error()
-    assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 0, 10, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 0, 99, None) == hip_kernels.UNSUPPORTED
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, 16, None, None, 16, 4, 8, 64, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_matmul_i32(MISALIGNED, 16, 16, 4, 8, 64, 0, None) == hip_kernels.MISALIGNED
-    assert library.chess_int8_matmul_i32(16, 16, 16, 4, 8, 64, 10, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_int8_matmul_i32(16, 16, 16, 4, 8, 64, 99, None) == hip_kernels.UNSUPPORTED
     attention = lambda *shape: library.chess_template_attention(16, 16, 16, 16, 16, *shape, 1e-5, 0.125, None)
     assert attention(1, 32, 8, 8, 64, 64, 8, 1) == hip_kernels.UNSUPPORTED            # fewer than 64 tokens
     assert attention(1, 70, 8, 3, 64, 64, 8, 1) == hip_kernels.INVALID_SHAPE           # 3 key/value heads for 8

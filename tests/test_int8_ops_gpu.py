@@ -138,7 +138,8 @@ def test_int8_linear_epilogues_match_the_oracle_to_the_bit(device, matmul, rows)
     operands = int8_operands(matmul, rows, device)
     x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
     expected = oracle_int8_linear(operands)
-    for tile in (1, 2):
+    table = (tile for tiles in INT8_TILES.values() for _, tile in tiles["down" if matmul.endswith("down") else matmul])
+    for tile in dict.fromkeys((1, 2, *table)):
         out = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
         assert out.dtype == torch.float16 and bits_equal(out, expected), tile
 
