@@ -87,27 +87,45 @@ DEVICE void lds_barrier() {
 template <int CH> DEVICE int swizzle(int row) { return CH >= 16 ? row % CH : (row / (16 / CH)) % CH; }
 template <int CH> DEVICE int raw_slot(int row, int chunk) { return row * CH + (chunk ^ swizzle<CH>(row)); }
 
-// Issue this wavefront's share of the DMA of rows [0, rows) of a raw block: row r's 16-byte chunk c from
-// source + min(r, last) * stride + 8 c halves into slot raw_slot(r, c). Rows past last read row last again (their
-// values are masked or multiplied by zero later), so every address is inside the projected rows.
-template <int CH>
-DEVICE void dma_rows(LDS_SPACE int8_t* raw, const half_t* source, int rows, int last, int stride, int wave, int waves, int lane) {
-    const int instructions = rows * CH / 64;
-    for (int i = wave; i < instructions; i += waves) {
-        const int slot = i * 64 + lane, row = slot / CH, chunk = (slot % CH) ^ swizzle<CH>(row);
-        const half_t* from = source + (size_t)min(row, last) * stride + chunk * 8;
-        __builtin_amdgcn_global_load_lds((const void*)from, (LDS_SPACE void*)(raw + i * 1024), 16, 0, 0);
+// A wavefront's share of the DMA of a raw block of ROWS rows x CH 16-byte chunks, 64 chunks an instruction:
+// instruction i = wave + j WAVES writes slots i * 64 + lane, slot s holding chunk (s % CH) ^ swizzle(row) of row
+// s / CH. The lane's source offsets (halves from the block's first column) are planned once: rows past last read
+// row last again (their values are masked or multiplied by zero later), so every address is inside the rows.
+template <int ROWS, int CH, int WAVES>
+struct DmaPlan {
+    static constexpr int INSTRUCTIONS = ROWS * CH / 64;
+    static constexpr int PER_WAVE = (INSTRUCTIONS + WAVES - 1) / WAVES;
+    static_assert(ROWS * CH % 64 == 0, "whole DMA instructions");
+    uint32_t offset[PER_WAVE];
+    DEVICE void plan(int last, int stride, int wave, int lane) {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; j++) {
+            const int slot = (wave + j * WAVES) * 64 + lane, row = min(slot / CH, ROWS - 1), chunk = (slot % CH) ^ swizzle<CH>(row);
+            offset[j] = (uint32_t)(min(row, last) * stride + chunk * 8);
+        }
     }
-}
+    DEVICE void issue(LDS_SPACE int8_t* raw, const half_t* source, int wave) const {
+#pragma unroll
+        for (int j = 0; j < PER_WAVE; j++) {
+            const int i = wave + j * WAVES;
+            if (INSTRUCTIONS % WAVES == 0 || i < INSTRUCTIONS)
+                __builtin_amdgcn_global_load_lds((const void*)(source + offset[j]), (LDS_SPACE void*)(raw + i * 1024), 16, 0, 0);
+        }
+    }
+};
 
+// TILES = ceil(T / 16) exactly: the launch picks the instantiation, so every count below is fixed at compile time.
+// Registers are held to two wavefronts a SIMD, within which no instantiation needs scratch: a scratch reload would
+// wait for the DMA in flight too. (Fewer registers for more workgroups a CU cost more instructions than they gain:
+// the kernel is bound by its VALU work.)
 template <int DQP, int DV, int TILES>
-__global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
+__global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2))) void template_attention_kernel(
     const half_t* __restrict__ projected, const half_t* __restrict__ keyed, const half_t* __restrict__ q_gain,
     const half_t* __restrict__ k_gain, half_t* __restrict__ out, int T, int heads, int kv_heads, int dq, int templates_count,
     int groups_per_block, float eps, float scale)
 {
     typedef Layout<DQP, DV, TILES> L;
-    constexpr int KC = L::KC, VC = L::VC;
+    constexpr int KC = L::KC, VC = L::VC, WAVES = TILES, THREADS = 64 * TILES, STEPS = L::STEPS, KEYS = L::KEYS;
     extern __shared__ __align__(16) int8_t lds[];
     half_t* keys = (half_t*)lds;
     half_t* values = (half_t*)(lds + L::KEYS_BYTES);
@@ -116,11 +134,8 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
     LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES;     // [2][per_kv][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
-    const int lane = threadIdx.x & 63, slab = threadIdx.x >> 6;
-    const int threads = blockDim.x, waves = threads / 64;
+    const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.y;
-    const int tiles = (T + 15) / 16;            // key tiles of the scores
-    const int steps = (tiles + 1) / 2;
     const int width = heads * dq + kv_heads * dq + kv_heads * DV + heads * templates_count;
     const int k_offset = heads * dq, v_offset = k_offset + kv_heads * dq, c_offset = v_offset + kv_heads * DV;
     const int per_kv = heads / kv_heads;
@@ -132,40 +147,45 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
     const bool query_ok = query < T;
     const bool square_query = query < 64;
 
-    // the first group's rows on their way while the templates and gains load
+    // the DMA plans: keys and queries share one (same rows, same chunks), values have their own
+    DmaPlan<KEYS, KC, WAVES> key_plan;
+    DmaPlan<STEPS * 32, VC, WAVES> value_plan;
+    key_plan.plan(T - 1, width, slab, lane);
+    value_plan.plan(T - 1, width, slab, lane);
+    const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
+
     auto dma_group = [&](int group, bool kv, bool q, int buffer) {
         if (kv) {
-            dma_rows<KC>(raw_k, board + k_offset + group * dq, tiles * 16, T - 1, width, slab, waves, lane);
-            dma_rows<VC>(raw_v, board + v_offset + group * DV, steps * 32, T - 1, width, slab, waves, lane);
+            key_plan.issue(raw_k, board + k_offset + group * dq, slab);
+            value_plan.issue(raw_v, board + v_offset + group * DV, slab);
         }
         if (q) {
             for (int hi = 0; hi < per_kv; hi++)
-                dma_rows<KC>(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, tiles * 16, T - 1, width,
-                             slab, waves, lane);
+                key_plan.issue(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, slab);
             if (templates_count == MAX_TEMPLATES) {
-                for (int hi = slab; hi < per_kv; hi += waves)
-                    __builtin_amdgcn_global_load_lds((const void*)(board + (size_t)lane * width + c_offset + (group * per_kv + hi) * MAX_TEMPLATES),
+                for (int hi = slab; hi < per_kv; hi += WAVES)
+                    __builtin_amdgcn_global_load_lds((const void*)(board + coefficient_row + (group * per_kv + hi) * MAX_TEMPLATES),
                                                      (LDS_SPACE void*)(raw_c + (buffer * per_kv + hi) * L::COEF_BYTES), 16, 0, 0);
             }
         }
     };
     dma_group(blockIdx.x * groups_per_block, true, true, 0);
 
-    // this lane's templates: keyed[query][16 kt + 4 quad + r][0..7], 4 f16 pairs a key
-    // (loaded unconditionally from clamped places, then zeroed, so that the loads issue together)
-    uint4 pairs[4][4];
-    const int template_query = min(query, 63);
+    // The template bias of a 16-key tile is an MFMA too: bias^T[k][q] = sum over (q', t) of templates[t][q'][k] *
+    // [q' == q] c[q][t], an inner dimension of the wavefront's 16 queries x 8 templates, 32 a step. In step j the A
+    // operand lane (key 16 kt + lane % 16, quad) holds keyed[q' = 16 slab + 4 j + quad][key][0..7] -- its query's 8
+    // templates for the key -- and the B operand lane (query col, quad) holds c[col][0..7] when 4 j + quad == col,
+    // else zeros. The A operands stay in registers for every group (zero for the queries past the squares; loaded
+    // from clamped places, then zeroed, so that the loads issue together).
+    uint4 templates[4][4];
 #pragma unroll
     for (int kt = 0; kt < 4; kt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++)
-            pairs[kt][r] = *reinterpret_cast<const uint4*>(keyed + ((size_t)template_query * 64 + kt * 16 + quad * 4 + r) * MAX_TEMPLATES);
-    if (!square_query) {
-#pragma unroll
-        for (int kt = 0; kt < 4; kt++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) pairs[kt][r] = uint4{0, 0, 0, 0};
-    }
+        for (int j = 0; j < 4; j++) {
+            const int template_query = slab * 16 + 4 * j + quad;
+            templates[kt][j] = *reinterpret_cast<const uint4*>(keyed + ((size_t)min(template_query, 63) * 64 + kt * 16 + (lane & 15)) * MAX_TEMPLATES);
+            if (template_query >= 64) templates[kt][j] = uint4{0, 0, 0, 0};
+        }
 
     half_t q_gains[DQP / 32][8];
 #pragma unroll
@@ -176,14 +196,22 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
             const half_t gain = q_gain[min(d, dq - 1)];
             q_gains[ks][e] = d < dq ? gain : (half_t)0.0f;
         }
-    // the key gains of the chunk this thread normalises (chunk threadIdx.x % KC of every key it takes)
+    // the keys this thread normalises: chunk tid % KC of keys tid / KC + k THREADS / KC (KC adjacent lanes a key)
+    constexpr int K_ITEMS = KEYS * KC / THREADS;
+    static_assert(KEYS * KC % THREADS == 0 && THREADS % KC == 0, "whole keys a pass");
+    const int k_chunk = tid % KC;
+    const bool k_chunk_ok = k_chunk * 8 < dq;
     half_t k_gains[8];
 #pragma unroll
     for (int e = 0; e < 8; e++) {
-        const int d = (threadIdx.x % KC) * 8 + e;
+        const int d = k_chunk * 8 + e;
         const half_t gain = k_gain[min(d, dq - 1)];
         k_gains[e] = d < dq ? gain : (half_t)0.0f;
     }
+    // the value pairs this thread transposes: key pair item % (STEPS 16), chunk item / (STEPS 16)
+    constexpr int V_TOTAL = STEPS * 16 * VC, V_ITEMS = (V_TOTAL + THREADS - 1) / THREADS;
+    // the staged outputs this thread writes out: row item / VC, chunk item % VC of each head
+    constexpr int O_TOTAL = KEYS * VC, O_ITEMS = (O_TOTAL + THREADS - 1) / THREADS;
     const float inverse_dq = 1.0f / (float)dq;
     // The templates and gains have landed before the loop (with the first group's rows): counting loads across the
     // loop's iterations, the compiler would otherwise wait for every load in flight -- the next group's rows too --
@@ -196,11 +224,17 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
     // Stored straight from the MFMA layout, 8 bytes a lane scattered over 16 rows, they would be waited for at once.
     constexpr bool STAGED = DV <= DQP;
     auto write_out = [&](int group, int buffer) {
-        constexpr int CHUNKS = DV / 8;
-        for (int item = threadIdx.x; item < per_kv * T * CHUNKS; item += threads) {
-            const int hi = item / (T * CHUNKS), rest = item % (T * CHUNKS), q = rest / CHUNKS, c = rest % CHUNKS;
-            const uint4 eight = lds_read16_settled(raw_q + (buffer * per_kv + hi) * head_bytes + raw_slot<KC>(q, c) * 16);
-            *reinterpret_cast<uint4*>(out + ((size_t)b * T + q) * (heads * DV) + (group * per_kv + hi) * DV + c * 8) = eight;
+        for (int hi = 0; hi < per_kv; hi++) {
+            const LDS_SPACE int8_t* staged = raw_q + (buffer * per_kv + hi) * head_bytes;
+            half_t* to = out + (size_t)b * T * (heads * DV) + (group * per_kv + hi) * DV;
+#pragma unroll
+            for (int k = 0; k < O_ITEMS; k++) {
+                const int item = tid + k * THREADS, q = item / VC, c = item % VC;
+                if ((O_TOTAL % THREADS == 0 || item < O_TOTAL) && q < T) {
+                    const uint4 eight = lds_read16_settled(staged + raw_slot<KC>(q, c) * 16);
+                    *reinterpret_cast<uint4*>(to + (size_t)q * (heads * DV) + c * 8) = eight;
+                }
+            }
         }
     };
 
@@ -215,10 +249,11 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
         if (gi + 1 < groups_per_block) dma_group(group + 1, false, true, buffer ^ 1);
 
         // keys, normalised with the gain: a thread a 16-byte chunk, KC adjacent lanes a key
-        for (int item = threadIdx.x; item < tiles * 16 * KC; item += threads) {
-            const int key = item / KC, c = item % KC;
-            v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(raw_k + raw_slot<KC>(key, c) * 16);
-            if (c * 8 >= dq) raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+        for (int k = 0; k < K_ITEMS; k++) {
+            const int key = tid / KC + k * (THREADS / KC);
+            v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(raw_k + raw_slot<KC>(key, k_chunk) * 16);
+            if (!k_chunk_ok) raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
             float squares = squares8(raw, 0.0f);
 #pragma unroll
             for (int offset = 1; offset < KC; offset <<= 1) squares += __shfl_xor(squares, offset, 64);
@@ -226,11 +261,14 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
             v8h normed;
 #pragma unroll
             for (int e = 0; e < 8; e++) normed[e] = (half_t)(((float)raw[e] * inverse) * (float)k_gains[e]);
-            *reinterpret_cast<v8h*>(keys + key * L::K_ROW + c * 8) = normed;
+            *reinterpret_cast<v8h*>(keys + key * L::K_ROW + k_chunk * 8) = normed;
         }
         // values, transposed to [d][key] a key pair at a time (4-byte writes)
-        for (int item = threadIdx.x; item < steps * 16 * VC; item += threads) {
-            const int kp = item % (steps * 16), c = item / (steps * 16), key = 2 * kp;
+#pragma unroll
+        for (int k = 0; k < V_ITEMS; k++) {
+            const int item = tid + k * THREADS;
+            if (V_TOTAL % THREADS != 0 && item >= V_TOTAL) break;
+            const int kp = item % (STEPS * 16), c = item / (STEPS * 16), key = 2 * kp;
             const v4u lo = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key, c) * 16);
             const v4u hi = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key + 1, c) * 16);
             const uint32_t lo_words[4] = {lo[0], lo[1], lo[2], lo[3]}, hi_words[4] = {hi[0], hi[1], hi[2], hi[3]};
@@ -248,7 +286,8 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
 
         for (int hi = 0; hi < per_kv; hi++) {
             const int head = group * per_kv + hi;
-            // this query's template coefficients for the head, as f16 pairs (zero past templates_count)
+            // this query's template coefficients for the head, as f16 pairs (zero past templates_count, and for the
+            // queries that are not squares, whose bias is then zero)
             uint4 coefficients;
             {
                 const half_t* from = board + (size_t)min(query, 63) * width + c_offset + head * templates_count;
@@ -286,35 +325,47 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
 #pragma unroll
                 for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)(((float)qv[ks][e] * q_inverse) * (float)q_gains[ks][e]);
 
-            // S^T tiles: lane holds s[query][16 kt + 4 quad + r]
-            float s[2 * L::STEPS][4];
+            // the bias MFMAs' B operands: this query's coefficients in the one step j with 4 j + quad == col
+            v8h mix[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+                mix[j] = __builtin_bit_cast(v8h, 4 * j + quad == col ? coefficients : uint4{0, 0, 0, 0});
+
+            // S^T tiles: lane holds s[query][16 kt + 4 quad + r]; square keys take the template bias (zero for the
+            // queries past the squares), keys past T are masked
+            float s[2 * STEPS][4];
             float top = -__builtin_inff();
 #pragma unroll
-            for (int kt = 0; kt < 2 * L::STEPS; kt++) {
-                if (kt >= TILES || kt >= tiles) {
+            for (int kt = 0; kt < 2 * STEPS; kt++) {
+                if (kt >= TILES) {
 #pragma unroll
                     for (int r = 0; r < 4; r++) s[kt][r] = -__builtin_inff();
                     continue;
                 }
+                // one tile's keys at a time: loads hoisted over the tiles would hold all their registers at once
+                __builtin_amdgcn_sched_barrier(0);
                 v4f acc = v4f{0, 0, 0, 0};
 #pragma unroll
                 for (int ks = 0; ks < DQP / 32; ks++) {
                     const v8h kf = *reinterpret_cast<const v8h*>(keys + (kt * 16 + col) * L::K_ROW + ks * 32 + quad * 8);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], acc, 0, 0, 0);
                 }
+                v4f bias = v4f{0, 0, 0, 0};
+                if (kt < 4) {
+#pragma unroll
+                    for (int j = 0; j < 4; j++)
+                        bias = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, templates[kt][j]), mix[j], bias, 0, 0, 0);
+                }
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    const int key = kt * 16 + quad * 4 + r;
                     float value = acc[r] * scale;
-                    if (kt < 4 && square_query) {
-                        float bias = dot2(coefficients.x, pairs[kt][r].x, 0.0f);
-                        bias = dot2(coefficients.y, pairs[kt][r].y, bias);
-                        bias = dot2(coefficients.z, pairs[kt][r].z, bias);
-                        bias = dot2(coefficients.w, pairs[kt][r].w, bias);
-                        value += (float)(half_t)bias;
+                    if (kt < 4) {
+                        value += (float)(half_t)bias[r];
+                    } else if (kt * 16 + quad * 4 + r >= T) {
+                        value = -__builtin_inff();
                     }
-                    s[kt][r] = kt < 4 || key < T ? value : -__builtin_inff();
-                    top = fmaxf(top, s[kt][r]);
+                    s[kt][r] = value;
+                    top = fmaxf(top, value);
                 }
             }
             top = fmaxf(top, __shfl_xor(top, 16, 64));
@@ -322,7 +373,7 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
             float total = 0.0f;
             const float offset = -top * LOG2E;
 #pragma unroll
-            for (int kt = 0; kt < 2 * L::STEPS; kt++)
+            for (int kt = 0; kt < 2 * STEPS; kt++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float p = kt < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], LOG2E, offset)) : 0.0f;
@@ -338,8 +389,8 @@ __global__ __launch_bounds__(64 * TILES) void template_attention_kernel(
 #pragma unroll
             for (int dt = 0; dt < DV / 16; dt++) o[dt] = v4f{0, 0, 0, 0};
 #pragma unroll
-            for (int st = 0; st < L::STEPS; st++) {
-                if (2 * st >= tiles) break;
+            for (int st = 0; st < STEPS; st++) {
+                __builtin_amdgcn_sched_barrier(0);
                 v8h pf;
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
@@ -395,7 +446,7 @@ int launch(const void* projected, const void* keyed, const void* q_gain, const v
         const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (allowed != hipSuccess) return (int)allowed;
     }
-    const dim3 grid(kv_heads / groups_per_block, B), block(64 * ((T + 15) / 16));
+    const dim3 grid(kv_heads / groups_per_block, B), block(64 * TILES);   // TILES == ceil(T / 16): the caller picked it so
     hipLaunchKernelGGL(kernel, grid, block, bytes, stream, (const half_t*)projected, (const half_t*)keyed, (const half_t*)q_gain,
                        (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale);
     return launch_status();
@@ -405,9 +456,13 @@ template <int DQP, int DV>
 int by_tokens(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
               int kv_heads, int dq, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
-    if (T <= 64) return launch<DQP, DV, 4>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-    if (T <= 80) return launch<DQP, DV, 5>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-    return launch<DQP, DV, 8>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+    switch ((T + 15) / 16) {
+        case 4: return launch<DQP, DV, 4>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 5: return launch<DQP, DV, 5>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 6: return launch<DQP, DV, 6>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 7: return launch<DQP, DV, 7>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        default: return launch<DQP, DV, 8>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+    }
 }
 
 template <int DQP>
