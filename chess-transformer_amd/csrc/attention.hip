@@ -58,18 +58,18 @@ struct Layout {
     static constexpr int STEPS = (TILES + 1) / 2;     // 32-key steps of P V
     static constexpr int KEYS = TILES * 16;           // keys (and queries) staged
     static constexpr int VKEYS = STEPS * 32;          // value keys staged (P is zero past T)
-    static constexpr int K_ROW = DQP + 8;             // halves a normalised key, padded against bank conflicts
     static constexpr int V_ROW = VKEYS + 8;           // halves a transposed value column: 8 mod 16, so that the
                                                       // transposing writes of key pairs spread over the banks
     static constexpr int KC = DQP / 8, VC = DV / 8;   // 16-byte chunks a raw key (query) row, a raw value row
-    // LDS in bytes: normalised keys, transposed values, raw keys, raw values, then two buffers of raw queries
-    static constexpr int KEYS_BYTES = KEYS * K_ROW * 2;
+    // LDS in bytes: transposed values, two buffers of raw keys, raw values, the keys' scales, then two buffers of
+    // raw queries and template coefficients
     static constexpr int VALUES_BYTES = DV * V_ROW * 2;
-    static constexpr int RAW_K_BYTES = KEYS * DQP * 2;
+    static constexpr int RAW_K_BYTES = KEYS * DQP * 2;   // a buffer's
     static constexpr int RAW_V_BYTES = VKEYS * DV * 2;
+    static constexpr int SCALES_BYTES = KEYS * 4;
     static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
     static constexpr int COEF_BYTES = 64 * MAX_TEMPLATES * 2;   // a head's template coefficients, a square query a row
-    static constexpr int FIXED_BYTES = KEYS_BYTES + VALUES_BYTES + RAW_K_BYTES + RAW_V_BYTES;
+    static constexpr int FIXED_BYTES = VALUES_BYTES + 2 * RAW_K_BYTES + RAW_V_BYTES + SCALES_BYTES;
     static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * (RAW_Q_BYTES + COEF_BYTES); }
 };
 
@@ -127,11 +127,11 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     typedef Layout<DQP, DV, TILES> L;
     constexpr int KC = L::KC, VC = L::VC, WAVES = TILES, THREADS = 64 * TILES, STEPS = L::STEPS, KEYS = L::KEYS;
     extern __shared__ __align__(16) int8_t lds[];
-    half_t* keys = (half_t*)lds;
-    half_t* values = (half_t*)(lds + L::KEYS_BYTES);
-    LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)(lds + L::KEYS_BYTES + L::VALUES_BYTES);
-    LDS_SPACE int8_t* raw_v = raw_k + L::RAW_K_BYTES;
-    LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES;     // [2][per_kv][KEYS * DQP halves]
+    half_t* values = (half_t*)lds;
+    LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)(lds + L::VALUES_BYTES);   // [2][KEYS * DQP halves]
+    LDS_SPACE int8_t* raw_v = raw_k + 2 * L::RAW_K_BYTES;
+    float* key_scales = (float*)(lds + L::VALUES_BYTES + 2 * L::RAW_K_BYTES + L::RAW_V_BYTES);   // [KEYS]: the scale times the key's rsqrt
+    LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES + L::SCALES_BYTES;     // [2][per_kv][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -154,12 +154,11 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     value_plan.plan(T - 1, width, slab, lane);
     const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
 
-    auto dma_group = [&](int group, bool kv, bool q, int buffer) {
-        if (kv) {
-            key_plan.issue(raw_k, board + k_offset + group * dq, slab);
-            value_plan.issue(raw_v, board + v_offset + group * DV, slab);
-        }
-        if (q) {
+    // a group's keys, queries and coefficients (into a buffer), or its values
+    auto dma_group = [&](int group, bool v, bool kq, int buffer) {
+        if (v) value_plan.issue(raw_v, board + v_offset + group * DV, slab);
+        if (kq) {
+            key_plan.issue(raw_k + buffer * L::RAW_K_BYTES, board + k_offset + group * dq, slab);
             for (int hi = 0; hi < per_kv; hi++)
                 key_plan.issue(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, slab);
             if (templates_count == MAX_TEMPLATES) {
@@ -187,27 +186,22 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             if (template_query >= 64) templates[kt][j] = uint4{0, 0, 0, 0};
         }
 
-    half_t q_gains[DQP / 32][8];
+    // The keys are not normalised in place: the scores are s = scale rsqrt_k sum_d (q_n[d] k_gain[d]) k[d], the query
+    // side taking both gains (f32 q_gain k_gain, zero past dq) and rounding to f16 once, the key side its raw f16 row
+    // and a per-key scale.
+    float gains[DQP / 32][8];
 #pragma unroll
     for (int ks = 0; ks < DQP / 32; ks++)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int d = ks * 32 + quad * 8 + e;
-            const half_t gain = q_gain[min(d, dq - 1)];
-            q_gains[ks][e] = d < dq ? gain : (half_t)0.0f;
+            const float gain = (float)q_gain[min(d, dq - 1)] * (float)k_gain[min(d, dq - 1)];
+            gains[ks][e] = d < dq ? gain : 0.0f;
         }
-    // the keys this thread normalises: chunk tid % KC of keys tid / KC + k THREADS / KC (KC adjacent lanes a key)
-    constexpr int K_ITEMS = KEYS * KC / THREADS;
-    static_assert(KEYS * KC % THREADS == 0 && THREADS % KC == 0, "whole keys a pass");
-    const int k_chunk = tid % KC;
-    const bool k_chunk_ok = k_chunk * 8 < dq;
-    half_t k_gains[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) {
-        const int d = k_chunk * 8 + e;
-        const half_t gain = k_gain[min(d, dq - 1)];
-        k_gains[e] = d < dq ? gain : (half_t)0.0f;
-    }
+    // the key scales: four adjacent threads a key, KC / 4 chunks each
+    constexpr int PART_CHUNKS = KC / 4;
+    static_assert(KEYS * 4 == THREADS && KC % 4 == 0, "four threads a key");
+    const int scale_key = tid / 4, first_chunk = (tid % 4) * PART_CHUNKS;
     // the value pairs this thread transposes: key pair item % (STEPS 16), chunk item / (STEPS 16)
     constexpr int V_TOTAL = STEPS * 16 * VC, V_ITEMS = (V_TOTAL + THREADS - 1) / THREADS;
     // the staged outputs this thread writes out: row item / VC, chunk item % VC of each head
@@ -248,20 +242,24 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
         if (STAGED && gi > 0) write_out(group - 1, buffer ^ 1);
         if (gi + 1 < groups_per_block) dma_group(group + 1, false, true, buffer ^ 1);
 
-        // keys, normalised with the gain: a thread a 16-byte chunk, KC adjacent lanes a key
+        // the keys' scales: scale * rsqrt(mean of squares + eps) over the key's dq columns. Past dq a raw key chunk
+        // holds another head's columns: zeroed here, as a zero query column would not cancel an infinite one.
+        {
+            LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
+            float squares = 0.0f;
 #pragma unroll
-        for (int k = 0; k < K_ITEMS; k++) {
-            const int key = tid / KC + k * (THREADS / KC);
-            v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(raw_k + raw_slot<KC>(key, k_chunk) * 16);
-            if (!k_chunk_ok) raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-            float squares = squares8(raw, 0.0f);
-#pragma unroll
-            for (int offset = 1; offset < KC; offset <<= 1) squares += __shfl_xor(squares, offset, 64);
-            const float inverse = __builtin_amdgcn_rsqf(squares * inverse_dq + eps);
-            v8h normed;
-#pragma unroll
-            for (int e = 0; e < 8; e++) normed[e] = (half_t)(((float)raw[e] * inverse) * (float)k_gains[e]);
-            *reinterpret_cast<v8h*>(keys + key * L::K_ROW + k_chunk * 8) = normed;
+            for (int c = 0; c < PART_CHUNKS; c++) {
+                LDS_SPACE int8_t* chunk = keys + raw_slot<KC>(scale_key, first_chunk + c) * 16;
+                v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(chunk);
+                if ((first_chunk + c) * 8 >= dq) {
+                    raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+                    *reinterpret_cast<LDS_SPACE v8h*>(chunk) = raw;
+                }
+                squares = squares8(raw, squares);
+            }
+            squares += lane_xor1(squares);
+            squares += lane_xor2(squares);
+            if (tid % 4 == 0) key_scales[scale_key] = __builtin_amdgcn_rsqf(squares * inverse_dq + eps) * scale;
         }
         // values, transposed to [d][key] a key pair at a time (4-byte writes)
 #pragma unroll
@@ -281,7 +279,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             }
         }
         lds_barrier();
-        // the raw keys and values are read: the next group's come in while this one's heads run
+        // the raw values are read: the next group's come in while this one's heads run
         if (gi + 1 < groups_per_block) dma_group(group + 1, true, false, 0);
 
         for (int hi = 0; hi < per_kv; hi++) {
@@ -307,6 +305,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             }
             // the query row's fragment of B: lane holds dq columns ks * 32 + 8 quad .. + 8
             const LDS_SPACE int8_t* queries = raw_q + (buffer * per_kv + hi) * head_bytes;
+            const LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
             v8h qv[DQP / 32];
             float squares = 0.0f;
 #pragma unroll
@@ -323,7 +322,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
             for (int ks = 0; ks < DQP / 32; ks++)
 #pragma unroll
-                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)(((float)qv[ks][e] * q_inverse) * (float)q_gains[ks][e]);
+                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)(((float)qv[ks][e] * q_inverse) * gains[ks][e]);
 
             // the bias MFMAs' B operands: this query's coefficients in the one step j with 4 j + quad == col
             v8h mix[4];
@@ -347,9 +346,10 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                 v4f acc = v4f{0, 0, 0, 0};
 #pragma unroll
                 for (int ks = 0; ks < DQP / 32; ks++) {
-                    const v8h kf = *reinterpret_cast<const v8h*>(keys + (kt * 16 + col) * L::K_ROW + ks * 32 + quad * 8);
+                    const v8h kf = *reinterpret_cast<const LDS_SPACE v8h*>(keys + raw_slot<KC>(kt * 16 + col, ks * 4 + quad) * 16);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], acc, 0, 0, 0);
                 }
+                const v4f key_scale = *reinterpret_cast<const v4f*>(key_scales + kt * 16 + quad * 4);
                 v4f bias = v4f{0, 0, 0, 0};
                 if (kt < 4) {
 #pragma unroll
@@ -358,7 +358,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                 }
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    float value = acc[r] * scale;
+                    float value = acc[r] * key_scale[r];
                     if (kt < 4) {
                         value += (float)(half_t)bias[r];
                     } else if (kt * 16 + quad * 4 + r >= T) {
