@@ -106,6 +106,32 @@ template <typename OutT> DEVICE void stage_four(OutT*, const float (&)[4]) {}
 constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 constexpr int LGKMCNT_ZERO = 0xC07F;
 
+// The DMA's buffer form: 16 bytes a lane from a buffer resource into LDS, the lane's offset from a VGPR and a
+// uniform offset from an SGPR, so that a load needs no address arithmetic in the lanes. The resource type exists in
+// the device pass only; the host pass, which only declares the kernels, gets an empty stand-in (given the type, it
+// silently emits no kernel stubs).
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufferResource;
+DEVICE BufferResource buffer_resource(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+DEVICE void buffer_dma16(BufferResource resource, LDS_SPACE void* to, uint32_t lane_offset, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(resource, to, 16, lane_offset, offset, 0, 0);
+}
+#else
+struct BufferResource {};
+DEVICE BufferResource buffer_resource(const void*, uint32_t) { return {}; }
+DEVICE void buffer_dma16(BufferResource, LDS_SPACE void*, uint32_t, uint32_t) {}
+#endif
+
+// f(std::integral_constant<int, I>) for I in [FIRST, LAST)
+template <int FIRST, int LAST, typename F> DEVICE void static_for(F&& f) {
+    if constexpr (FIRST < LAST) {
+        f(std::integral_constant<int, FIRST>{});
+        static_for<FIRST + 1, LAST>(f);
+    }
+}
+
 DEVICE void bare_barrier() {
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
@@ -226,9 +252,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         return HALVES == 1 ? staged_row : staged_row / HALF_ROWS * WM + pass / HALF_PASSES * HALF_ROWS + staged_row % HALF_ROWS;
     };
     constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
+    // prefetched while they fit beside the sums (8 passes, 64 registers at most); else read in phase 2
+    constexpr bool PREFETCH = ADDS && PASSES <= 8;
     const bool vectors = N % 8 == 0;
-    v8h residual_rows[ADDS ? PASSES : 1], original_rows[ADDS ? PASSES : 1];
-    if constexpr (ADDS) {
+    v8h residual_rows[PREFETCH ? PASSES : 1], original_rows[PREFETCH ? PASSES : 1];
+    if constexpr (PREFETCH) {
 #pragma unroll
         for (int pass = 0; pass < PASSES; pass++) {
             const size_t at = (size_t)min(m0 + pass_row(pass), M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
@@ -238,14 +266,18 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     }
 
     LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
-    auto issue = [&](int step) {
+    // The operands as buffer resources: a DMA load takes the lane's offset from a VGPR and the step's K offset from an
+    // SGPR, with no address arithmetic in the lanes. (The host keeps both operands under 4 GiB.)
+    const BufferResource x_rsrc = buffer_resource(x, (uint32_t)M * (uint32_t)row_bytes);
+    const BufferResource w_rsrc = buffer_resource(w, (uint32_t)NB * (uint32_t)N * (uint32_t)row_bytes);
+    // the DMA of step into ring stage S (S == step % STAGES, fixed at compile time)
+    auto issue = [&](int step, auto stage_index) {
+        constexpr int S = decltype(stage_index)::value;
         const int k0 = min(step, steps - 1) * STAGE_K_BYTES;
-        LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
 #pragma unroll
-        for (int p = 0; p < PER_WAVE; p++) {
-            const int8_t* base = (wave * PER_WAVE + p < A_BLOCKS ? (const int8_t*)x : (const int8_t*)w) + k0;
-            __builtin_amdgcn_global_load_lds((const void*)(base + source[p]), (LDS_SPACE void*)(stage + (wave * PER_WAVE + p) * BLOCK), 16, 0, 0);
-        }
+        for (int p = 0; p < PER_WAVE; p++)
+            buffer_dma16(wave * PER_WAVE + p < A_BLOCKS ? x_rsrc : w_rsrc, (LDS_SPACE void*)(ring + S * STAGE_BYTES + (wave * PER_WAVE + p) * BLOCK),
+                         source[p], k0);
     };
 
     typename MMA::Acc acc[NB][FM][FN];
@@ -253,42 +285,54 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     // an operand lane (row lane % 32, 16-byte half lane / 32 of each 32-byte sub-step) in a stage: the block of its
     // 16 rows, then the slot 4 r + (chunk ^ (r / 4)) of row r's chunk
     const int in_row = lane & 31, half = lane >> 5, r16 = in_row & 15;
-    int operand[2];
+    // a lane's operand addresses in stage 0: this wavefront's A rows and B columns (the fragment and stage offsets
+    // are then immediates)
+    int a_operand[2], b_operand[2];
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++) operand[sub] = (in_row >> 4) * BLOCK + (r16 * 4 + ((half + 2 * sub) ^ (r16 >> 2))) * 16;
+    for (int sub = 0; sub < 2; sub++) {
+        const int operand = (in_row >> 4) * BLOCK + (r16 * 4 + ((half + 2 * sub) ^ (r16 >> 2))) * 16;
+        a_operand[sub] = operand + (wm * WM / 16) * BLOCK;
+        b_operand[sub] = operand + (A_BLOCKS + wn * WN / 16) * BLOCK;
+    }
 
-#pragma unroll
-    for (int s = 0; s < STAGES - 1; s++) issue(s);
+    static_for<0, STAGES - 1>([&](auto s) { issue(decltype(s)::value, s); });
     // a step's MFMAs; the first step's start from zero sums (the MFMA's zero accumulator operand), so nothing clears them
-    auto multiply = [&](const LDS_SPACE int8_t* stage, auto first_step) {
+    auto multiply = [&](auto stage_index, auto first_step) {
         constexpr bool FIRST = decltype(first_step)::value;
+        constexpr int STAGE = decltype(stage_index)::value * STAGE_BYTES;
 #pragma unroll
         for (int sub = 0; sub < 2; sub++) {
             typename MMA::Operand af[FM];
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                af[i] = *(const LDS_SPACE typename MMA::Operand*)(stage + ((wm * WM + i * 32) / 16) * BLOCK + operand[sub]);
+                af[i] = *(const LDS_SPACE typename MMA::Operand*)(ring + a_operand[sub] + STAGE + (i * 32 / 16) * BLOCK);
 #pragma unroll
             for (int g = 0; g < NB; g++)
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     const typename MMA::Operand bf =
-                        *(const LDS_SPACE typename MMA::Operand*)(stage + (A_BLOCKS + (g * BN + wn * WN + j * 32) / 16) * BLOCK + operand[sub]);
+                        *(const LDS_SPACE typename MMA::Operand*)(ring + b_operand[sub] + STAGE + ((g * BN + j * 32) / 16) * BLOCK);
 #pragma unroll
                     for (int i = 0; i < FM; i++)
                         acc[g][i][j] = MMA::step(bf, af[i], FIRST && sub == 0 ? typename MMA::Acc{} : acc[g][i][j]);
                 }
         }
     };
-    for (int step = 0; step < steps; step++) {
+    // a step: its stage landed and the stage it refills read by every wavefront; the DMA STAGES - 1 steps ahead (past
+    // the end it loads the last step again); its MFMAs
+    auto run_step = [&](int step, auto stage_index, auto first_step) {
+        constexpr int S = decltype(stage_index)::value;
         stage_barrier<PER_WAVE * (STAGES - 2)>();
-        issue(step + STAGES - 1);   // into the stage read one step ago; past the end it loads the last step again
-        const LDS_SPACE int8_t* stage = ring + (step % STAGES) * STAGE_BYTES;
-        if (step == 0) {
-            multiply(stage, std::true_type{});
-        } else {
-            multiply(stage, std::false_type{});
-        }
+        issue(step + STAGES - 1, std::integral_constant<int, (S + STAGES - 1) % STAGES>{});
+        multiply(stage_index, first_step);
+    };
+    // step 0 (its MFMAs start from zero sums), then STAGES steps a turn, so that every stage offset is an immediate
+    run_step(0, std::integral_constant<int, 0>{}, std::true_type{});
+    for (int turn = 1; turn < steps; turn += STAGES) {
+        static_for<0, STAGES>([&](auto s) {
+            if (turn + decltype(s)::value < steps)
+                run_step(turn + decltype(s)::value, std::integral_constant<int, (1 + decltype(s)::value) % STAGES>{}, std::false_type{});
+        });
     }
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
     // the prefetched raw bits are first touched here, so that nothing converts (and waits for) them before the loop
@@ -405,7 +449,8 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                 if (flags & EPI_RESIDUAL) {
                     if (vectors) {
 #pragma unroll
-                        for (int c = 0; c < 8; c++) value[c] = value[c] + (float)residual_rows[ADDS ? pass : 0][c];
+                        for (int c = 0; c < 8; c++)
+                            value[c] = value[c] + (float)(PREFETCH ? residual_rows[PREFETCH ? pass : 0] : *reinterpret_cast<const v8h*>(e.residual + at))[c];
                     } else {
 #pragma unroll
                         for (int c = 0; c < 8; c++)
@@ -416,7 +461,8 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                     float original[8];
                     if (vectors) {
 #pragma unroll
-                        for (int c = 0; c < 8; c++) original[c] = (float)original_rows[ADDS ? pass : 0][c];
+                        for (int c = 0; c < 8; c++)
+                            original[c] = (float)(PREFETCH ? original_rows[PREFETCH ? pass : 0] : *reinterpret_cast<const v8h*>(e.original + at))[c];
                     } else {
 #pragma unroll
                         for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
@@ -478,7 +524,7 @@ template <typename In, int NB, typename OutT>
 int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     if (tile == 0) {
         const long large = (long)((M + 255) / 256) * ((N + 127) / 128);
-        tile = large >= 512 ? 4 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
+        tile = large >= 512 ? 11 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
     }
     // the network's epilogues are built with their flags fixed; any other combination reads them at run time
     const int f = e.flags;
