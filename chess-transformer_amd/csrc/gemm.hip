@@ -33,8 +33,13 @@
 // back by rows, so that residual, input embedding and outputs move 16 bytes a lane with a row's columns
 // contiguous across lanes.
 #include "chess_common.h"
+#include "lds_dma.h"
 
 #include <type_traits>
+
+// gemm_stream.hip: the persistent gated GEMM (tile 12)
+int launch_gated_stream(const void* x, const void* w, void* out, const float* x_scale, const float* w_scale, int M, int N, int K,
+                        hipStream_t stream);
 
 namespace {
 
@@ -57,7 +62,6 @@ struct Epilogue {
 
 typedef int v16i __attribute__((ext_vector_type(16)));
 typedef float v16f __attribute__((ext_vector_type(16)));
-#define LDS_SPACE __attribute__((address_space(3)))
 
 template <typename In> struct Mfma;
 template <> struct Mfma<int8_t> {
@@ -74,7 +78,6 @@ template <> struct Mfma<half_t> {
 };
 
 // outputs are streamed (non-temporal stores), so that they do not push the operands out of L2
-typedef unsigned v4u __attribute__((ext_vector_type(4)));
 template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
 template <> DEVICE void store_eight<half_t>(half_t* to, const float (&v)[8]) {
     const v8h eight = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
@@ -101,49 +104,6 @@ template <> DEVICE void stage_four<bf16_t>(bf16_t* to, const float (&v)[4]) {
     *reinterpret_cast<uint2*>(to) = uint2{lo, hi};
 }
 template <typename OutT> DEVICE void stage_four(OutT*, const float (&)[4]) {}
-
-// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding)
-constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
-constexpr int LGKMCNT_ZERO = 0xC07F;
-
-// The DMA's buffer form: 16 bytes a lane from a buffer resource into LDS, the lane's offset from a VGPR and a
-// uniform offset from an SGPR, so that a load needs no address arithmetic in the lanes. The resource type exists in
-// the device pass only; the host pass, which only declares the kernels, gets an empty stand-in (given the type, it
-// silently emits no kernel stubs).
-#if defined(__HIP_DEVICE_COMPILE__)
-typedef __amdgpu_buffer_rsrc_t BufferResource;
-DEVICE BufferResource buffer_resource(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-DEVICE void buffer_dma16(BufferResource resource, LDS_SPACE void* to, uint32_t lane_offset, uint32_t offset) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(resource, to, 16, lane_offset, offset, 0, 0);
-}
-#else
-struct BufferResource {};
-DEVICE BufferResource buffer_resource(const void*, uint32_t) { return {}; }
-DEVICE void buffer_dma16(BufferResource, LDS_SPACE void*, uint32_t, uint32_t) {}
-#endif
-
-// f(std::integral_constant<int, I>) for I in [FIRST, LAST)
-template <int FIRST, int LAST, typename F> DEVICE void static_for(F&& f) {
-    if constexpr (FIRST < LAST) {
-        f(std::integral_constant<int, FIRST>{});
-        static_for<FIRST + 1, LAST>(f);
-    }
-}
-
-DEVICE void bare_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Every wavefront's DMA loads of the stage to be read have landed and every wavefront is done reading the
-// stage the next DMA overwrites. The compiler fences of __syncthreads would wait for all loads in flight.
-template <int OUTSTANDING> DEVICE void stage_barrier() {
-    __builtin_amdgcn_s_waitcnt(vmcnt_only(OUTSTANDING) & ~(0xF << 8));   // and lgkmcnt(0): this wavefront's reads are done
-    bare_barrier();
-}
 
 // An f32 staged tile (an epilogue that still adds to it) is staged half its rows at a time when every wavefront
 // has two or more row fragments: half the LDS, so that more workgroups fit a CU.
@@ -495,13 +455,14 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
     return launch_status();
 }
 
-constexpr int TILES = 11;
+constexpr int TILES = 12;
 
 // The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
 // 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
 // 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2). 0 picks by the launch's size.
+// 12 is the persistent gated GEMM of gemm_stream.hip (256 x 64, a 4-stage ring running across tiles), gated fp16 only.
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
@@ -528,6 +489,12 @@ int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, 
     }
     // the network's epilogues are built with their flags fixed; any other combination reads them at run time
     const int f = e.flags;
+    if (tile == 12) {
+        if constexpr (std::is_same<In, int8_t>::value && NB == 2 && std::is_same<OutT, half_t>::value) {
+            if (f == 0) return launch_gated_stream(x, w, out, e.x_scale, e.w_scale, M, N, K, stream);
+        }
+        return chess_fail(CHESS_UNSUPPORTED, "tile 12 is the streamed gated GEMM: int8 in, fp16 out, gated, no bias or residual");
+    }
     if constexpr (std::is_same<OutT, half_t>::value) {
         if (NB == 2 && f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);
         if (NB == 1 && f == EPI_BIAS) return by_tile<In, NB, OutT, true, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);

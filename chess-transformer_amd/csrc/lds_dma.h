@@ -1,0 +1,66 @@
+// LDS staging by DMA for the gfx950 GEMM kernels: explicit vmcnt waits, barriers that leave the DMA in flight,
+// buffer-resource loads straight into LDS, and compile-time loops over ring stages.
+#pragma once
+
+#include "chess_common.h"
+
+#include <type_traits>
+
+#define LDS_SPACE __attribute__((address_space(3)))
+
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+typedef unsigned v4u __attribute__((ext_vector_type(4)));
+
+// s_waitcnt with vmcnt = n and the other counters left alone (gfx9 encoding)
+constexpr int vmcnt_only(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int LGKMCNT_ZERO = 0xC07F;
+
+// The DMA's buffer form: 16 bytes a lane from a buffer resource into LDS, the lane's offset from a VGPR and a
+// uniform offset from an SGPR, so that a load needs no address arithmetic in the lanes. The resource type exists in
+// the device pass only; the host pass, which only declares the kernels, gets an empty stand-in (given the type, it
+// silently emits no kernel stubs).
+#if defined(__HIP_DEVICE_COMPILE__)
+typedef __amdgpu_buffer_rsrc_t BufferResource;
+DEVICE BufferResource buffer_resource(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+DEVICE void buffer_dma16(BufferResource resource, LDS_SPACE void* to, uint32_t lane_offset, uint32_t offset) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(resource, to, 16, lane_offset, offset, 0, 0);
+}
+// 8 bytes a lane to a buffer (cached: scattered 8-byte stores rely on L2 to merge them into lines); a lane whose
+// offset is past the resource's bytes stores nothing
+DEVICE void buffer_store8(BufferResource resource, uint2 value, uint32_t lane_offset, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(v2u, value), resource, lane_offset, offset, 0);
+}
+// 16 bytes a lane to a buffer, streamed (non-temporal: whole rows of outputs that do not push the operands out of L2)
+DEVICE void buffer_store16_streamed(BufferResource resource, v4u value, uint32_t lane_offset, uint32_t offset) {
+    __builtin_amdgcn_raw_buffer_store_b128(value, resource, lane_offset, offset, 2);
+}
+#else
+struct BufferResource {};
+DEVICE BufferResource buffer_resource(const void*, uint32_t) { return {}; }
+DEVICE void buffer_dma16(BufferResource, LDS_SPACE void*, uint32_t, uint32_t) {}
+DEVICE void buffer_store8(BufferResource, uint2, uint32_t, uint32_t) {}
+DEVICE void buffer_store16_streamed(BufferResource, v4u, uint32_t, uint32_t) {}
+#endif
+
+// f(std::integral_constant<int, I>) for I in [FIRST, LAST)
+template <int FIRST, int LAST, typename F> DEVICE void static_for(F&& f) {
+    if constexpr (FIRST < LAST) {
+        f(std::integral_constant<int, FIRST>{});
+        static_for<FIRST + 1, LAST>(f);
+    }
+}
+
+DEVICE void bare_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Every wavefront's DMA loads of the stage to be read have landed and every wavefront is done reading the
+// stage the next DMA overwrites. The compiler fences of __syncthreads would wait for all loads in flight.
+template <int OUTSTANDING> DEVICE void stage_barrier() {
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(OUTSTANDING) & ~(0xF << 8));   // and lgkmcnt(0): this wavefront's reads are done
+    bare_barrier();
+}

@@ -157,6 +157,29 @@ def test_the_gated_epilogue_is_silu_times_up(device, rows):
         assert torch.equal(out, first)
 
 
+@pytest.mark.parametrize("rows, width", [(70, 128), (1000, 2048), (4096, 2048), (71680, 2048)])
+def test_the_streamed_gated_gemm_gives_the_tiled_kernels_bits(device, rows, width):
+    """Tile 12, the persistent gated GEMM: a partial last row block (1000), an even and an odd count of tiles a
+    workgroup (4096, 71680 rows: 2 and 35), the network's batch-1024 shape (71680 x 2048 from 512)."""
+    operands = int8_operands("gate_up", rows, device, width=width, depth=512)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    tiled = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 2)
+    streamed = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)
+    assert torch.equal(streamed, tiled)
+    if rows * width <= 70 * 128:
+        expected = oracle_int8_linear(operands).astype(np.float64)
+        assert np.allclose(cpu(streamed).astype(np.float64), expected, atol=1e-3, rtol=2e-3)
+
+
+def test_the_streamed_gated_gemm_refuses_what_it_cannot_take(device):
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("gate_up", 70, device, width=200, depth=512)
+    with pytest.raises(ValueError):
+        launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)   # N not a multiple of 64
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("projection", 70, device, width=128, depth=512)
+    with pytest.raises(ValueError):
+        launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)   # not gated
+
+
 def dequantised(integers: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     return integers.double() * scale.double()[:, None]
 
