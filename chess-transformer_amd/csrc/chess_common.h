@@ -61,22 +61,56 @@ DEVICE float silu_fast(float g) {
 DEVICE float lane_xor1(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); }
 DEVICE float lane_xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)); }
 
-// xor butterflies over the 64 lanes of a wavefront: every lane ends with the same bits,
-// the balanced tree of adjacent lane pairs (a + b == b + a bitwise).
+// lane 7 - i and lane 15 - i of each 8 and 16 lanes by DPP mirrors (row_half_mirror, row_mirror)
+DEVICE float lane_mirror8(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)); }
+DEVICE float lane_mirror16(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); }
+DEVICE float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
+
+// The balanced tree of adjacent lane pairs over the 64 lanes of a wavefront, every lane ending with the same bits
+// (a + b == b + a bitwise): pairs of lanes, of 2, 4 and 8 lanes, then of 16-lane rows. Once a group's lanes all hold
+// its partial, pairing lane i with 7 - i or 15 - i (DPP mirrors) adds the same two partials as lane i ^ 4 or i ^ 8;
+// the four rows' sums are then added as (r0 + r1) + (r2 + r3). VALU only: no LDS permutes.
 DEVICE float wave_sum(float v) {
     v = v + lane_xor1(v);
     v = v + lane_xor2(v);
-#pragma unroll
-    for (int offset = 4; offset < 64; offset <<= 1) v = v + __shfl_xor(v, offset, 64);
-    return v;
+    v = v + lane_mirror8(v);
+    v = v + lane_mirror16(v);
+    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
 }
 
 DEVICE float wave_max(float v) {
     v = fmaxf(v, lane_xor1(v));
     v = fmaxf(v, lane_xor2(v));
+    v = fmaxf(v, lane_mirror8(v));
+    v = fmaxf(v, lane_mirror16(v));
+    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+}
+
+// One row of norm_quant's declared order on a wavefront, C contiguous elements a lane (zeros past the row's D):
+// the lane's squares as a pairwise tree, the wavefront's balanced tree (wave_sum), y = (v * (1 / sqrt(total / D + eps)))
+// * gain, absmax = max(max |y|, 1e-20), q = rint(y * (127 / absmax)). Returns absmax (the row's scale is absmax / 127).
+template <int C> DEVICE float norm_quant_row(const float (&v)[C], const float (&gain)[C], int D, float eps, int8_t (&q)[C]) {
+    float squares[C];
 #pragma unroll
-    for (int offset = 4; offset < 64; offset <<= 1) v = fmaxf(v, __shfl_xor(v, offset, 64));
-    return v;
+    for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
+#pragma unroll
+    for (int width = C; width > 1; width >>= 1)
+#pragma unroll
+        for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
+    const float total = wave_sum(squares[0]);
+    const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + eps);
+    float y[C];
+    float largest = 0.0f;
+#pragma unroll
+    for (int i = 0; i < C; i++) {
+        y[i] = (v[i] * inverse) * gain[i];
+        largest = fmaxf(largest, fabsf(y[i]));
+    }
+    const float absmax = fmaxf(wave_max(largest), 1e-20f);
+    const float inverse_step = 127.0f / absmax;
+#pragma unroll
+    for (int i = 0; i < C; i++) q[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
+    return absmax;
 }
 
 // Maps a workgroup id so that consecutive tiles land on one XCD: the hardware deals

@@ -5,7 +5,7 @@
 //   absmax = max(max |y|, 1e-20);  q = rint(y * (127 / absmax));  scale = absmax / 127
 // A wavefront takes R rows, one at a time, after loading all of them; a lane holds C = next_pow2(D) / 64
 // contiguous elements of a row (at least 1), sums its squares as a pairwise tree and the wavefront adds
-// the lanes' sums by xor butterflies, which is the balanced tree over the zero-padded row.
+// the lanes' sums as a balanced tree of adjacent lanes, which is the balanced tree over the zero-padded row.
 // Bandwidth-bound: 16-byte loads and stores, R rows of loads in flight a wavefront.
 #include "chess_common.h"
 
@@ -104,29 +104,8 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
             }
         }
 
-        // the lane's squares as a pairwise tree, then the wavefront's butterflies
-        float squares[C];
-#pragma unroll
-        for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
-#pragma unroll
-        for (int width = C; width > 1; width >>= 1)
-#pragma unroll
-            for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
-        const float total = wave_sum(squares[0]);
-        const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + eps);
-
-        float y[C];
-        float largest = 0.0f;
-#pragma unroll
-        for (int i = 0; i < C; i++) {
-            y[i] = (v[i] * inverse) * g[i];
-            largest = fmaxf(largest, fabsf(y[i]));
-        }
-        const float absmax = fmaxf(wave_max(largest), 1e-20f);
-        const float inverse_step = 127.0f / absmax;
         int8_t out[C];
-#pragma unroll
-        for (int i = 0; i < C; i++) out[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
+        const float absmax = norm_quant_row<C>(v, g, D, eps, out);
         if (vector) {
             if (col < D) copy_bytes<C>(q + base + col, out);
         } else {
