@@ -47,7 +47,7 @@ constexpr int STAGE_K_BYTES = 64;
 constexpr int THREADS = 256;
 constexpr int BLOCK = 1024;      // bytes a DMA instruction writes: 16 rows x 64 bytes
 
-enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4 };
+enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4, EPI_NORM = 8 };
 
 struct Epilogue {
     const float* x_scale;        // int8 only
@@ -58,6 +58,11 @@ struct Epilogue {
     const half_t* residual_scale;
     const half_t* input_scale;
     int flags;
+    // EPI_NORM (whole-row tiles only): the fp16 output rows also leave as norm_quant's q[M, N] and scale[M]
+    const half_t* norm_gain;
+    int8_t* norm_q;
+    float* norm_scale;
+    float norm_eps;
 };
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -202,6 +207,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
     }
     constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = BM / ROWS;
+    // EPI_NORM: a wavefront's phase-2 pass holds one whole output row, 8 columns a lane, the layout norm_quant takes
+    constexpr bool NORM = EPI >= 0 && (EPI & EPI_NORM);
+    static_assert(!NORM || (ROW_LANES == 64 && !RAW && !PACKED && std::is_same<OutT, half_t>::value), "a normalised row is one wavefront's");
+    v4u gain_bits = {0u, 0u, 0u, 0u};   // the lane's 8 gains, raw
+    if constexpr (NORM) gain_bits = *reinterpret_cast<const v4u*>(e.norm_gain + lane * 8);
     // Staged in halves, half h holds row fragments h * HALF_FM .. of every wavefront: staged row r is tile row
     // (r / HALF_ROWS) * WM + h * HALF_ROWS + r % HALF_ROWS.
     constexpr int HALVES = staging_halves<BM, WAVES_M, PACKED>(), HALF_FM = FM / HALVES, HALF_ROWS = WM / HALVES;
@@ -212,17 +222,24 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         return HALVES == 1 ? staged_row : staged_row / HALF_ROWS * WM + pass / HALF_PASSES * HALF_ROWS + staged_row % HALF_ROWS;
     };
     constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
-    // prefetched while they fit beside the sums (8 passes, 64 registers at most); else read in phase 2
+    // The residual / original rows of phase 2, held in registers: all of them loaded now while they fit beside the sums
+    // (8 passes, 64 registers at most); in the whole-row tile (16 passes, staged in halves), the first half's rows now and
+    // the second half's once the first half is staged (its sums then dead). A pass's own loads would wait: they cannot
+    // move above the previous pass's stores, which the compiler cannot tell apart from them. (The other tiles of more
+    // than 8 passes read in phase 2: with held rows the compiler fails on the gated 256 x 128 tile.)
     constexpr bool PREFETCH = ADDS && PASSES <= 8;
+    constexpr bool AHEAD = NORM && HALVES == 2 && HALF_PASSES <= 8;
+    constexpr bool HELD = PREFETCH || AHEAD;
     const bool vectors = N % 8 == 0;
-    v8h residual_rows[PREFETCH ? PASSES : 1], original_rows[PREFETCH ? PASSES : 1];
-    if constexpr (PREFETCH) {
+    v8h residual_rows[HELD ? PASSES : 1], original_rows[HELD ? PASSES : 1];
+    auto load_rows = [&](int pass) {
+        const size_t at = (size_t)min(m0 + pass_row(pass), M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
+        if (vectors && (flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
+        if (vectors && (flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
+    };
+    if constexpr (HELD) {
 #pragma unroll
-        for (int pass = 0; pass < PASSES; pass++) {
-            const size_t at = (size_t)min(m0 + pass_row(pass), M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
-            if (vectors && (flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
-            if (vectors && (flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
-        }
+        for (int pass = 0; pass < (PREFETCH ? PASSES : HALF_PASSES); pass++) load_rows(pass);
     }
 
     LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
@@ -299,6 +316,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
     asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
+    if constexpr (NORM) asm volatile("" : "+v"(gain_bits));
     float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>());
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++)
@@ -370,6 +388,12 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         }
         __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
         bare_barrier();
+        if constexpr (AHEAD) {
+            if (h == 0) {
+#pragma unroll
+                for (int pass = HALF_PASSES; pass < PASSES; pass++) load_rows(pass);
+            }
+        }
 
         // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
         // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
@@ -410,7 +434,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                     if (vectors) {
 #pragma unroll
                         for (int c = 0; c < 8; c++)
-                            value[c] = value[c] + (float)(PREFETCH ? residual_rows[PREFETCH ? pass : 0] : *reinterpret_cast<const v8h*>(e.residual + at))[c];
+                            value[c] = value[c] + (float)(HELD ? residual_rows[HELD ? pass : 0] : *reinterpret_cast<const v8h*>(e.residual + at))[c];
                     } else {
 #pragma unroll
                         for (int c = 0; c < 8; c++)
@@ -422,13 +446,29 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
                     if (vectors) {
 #pragma unroll
                         for (int c = 0; c < 8; c++)
-                            original[c] = (float)(PREFETCH ? original_rows[PREFETCH ? pass : 0] : *reinterpret_cast<const v8h*>(e.original + at))[c];
+                            original[c] = (float)(HELD ? original_rows[HELD ? pass : 0] : *reinterpret_cast<const v8h*>(e.original + at))[c];
                     } else {
 #pragma unroll
                         for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
                     }
 #pragma unroll
                     for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
+                }
+                if constexpr (NORM) {
+                    // norm_quant of the row as stored: the fp16-rounded values (the row is the wavefront's, m the same in every lane)
+                    const v8h gain = __builtin_bit_cast(v8h, gain_bits);
+                    float stored[8], g[8];
+                    int8_t q8[8];
+#pragma unroll
+                    for (int c = 0; c < 8; c++) {
+                        stored[c] = (float)(half_t)value[c];
+                        g[c] = (float)gain[c];
+                    }
+                    const float absmax = norm_quant_row<8>(stored, g, N, e.norm_eps, q8);
+                    store_eight<OutT>(out + at, value);
+                    *reinterpret_cast<v2u*>(e.norm_q + at) = __builtin_bit_cast(v2u, q8);
+                    if (lane == 0) e.norm_scale[m] = absmax / 127.0f;
+                    continue;
                 }
                 if (vectors) {
                     store_eight<OutT>(out + at, value);
@@ -508,6 +548,22 @@ int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, 
     return by_tile<In, NB, OutT, false, -1>(x, w, out, e, M, N, K, tile, stream);
 }
 
+// EPI_NORM's whole-row tile: 64 rows x 512 outputs, 1 x 4 wavefronts, 2 stages (76 KB of LDS, so two workgroups a
+// CU); phase 2 gives each wavefront one whole row a pass.
+constexpr int NORM_WIDTH = 512;
+template <typename In, int EPI>
+int launch_normalised(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
+    static_assert(EPI & EPI_NORM, "the whole-row tile is for the normalising epilogue");
+    return launch<In, 64, NORM_WIDTH, 1, 4, 1, 2, half_t, false, EPI>(x, w, out, e, M, N, K, stream);
+}
+
+int check_norm(const void* residual, const void* gain, const void* q, const void* scale, int N, const char* what) {
+    if (!residual || !gain || !q || !scale) return chess_fail(CHESS_INVALID_SHAPE, "%s needs the residual, the gain, q and scale", what);
+    if (N != NORM_WIDTH) return chess_fail(CHESS_UNSUPPORTED, "%s normalises rows of %d outputs, not %d", what, NORM_WIDTH, N);
+    if (!aligned16(gain) || !aligned16(q)) return chess_fail(CHESS_MISALIGNED, "%s reads the gain and writes q 16 and 8 bytes a lane", what);
+    return CHESS_OK;
+}
+
 int check(const void* x, const void* w, void* out, int M, int N, int K, int depth, int tile, const char* what) {
     if (M < 0 || N <= 0 || K <= 0) return chess_fail(CHESS_INVALID_SHAPE, "%s: M %d, N %d, K %d", what, M, N, K);
     if (K % depth != 0) return chess_fail(CHESS_INVALID_SHAPE, "%s reads the %d inputs %d at a time", what, K, depth);
@@ -576,4 +632,35 @@ extern "C" int chess_linear(const void* x, const void* w, const void* bias, cons
                                     : dispatch<half_t, 2, float>(x, w, out, e, M, N, K, tile, s);
     }
     return out_dtype == OUT_F16 ? dispatch<half_t, 1, half_t>(x, w, out, e, M, N, K, tile, s) : dispatch<half_t, 1, float>(x, w, out, e, M, N, K, tile, s);
+}
+
+extern "C" int chess_linear_norm_quant(const void* x, const void* w, const void* bias, const void* residual, const void* gain, void* out,
+                                       void* q, void* scale, int M, int N, int K, float eps, void* stream)
+{
+    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES / 2, 0, "linear_norm_quant")) return status;
+    if (int status = check_epilogue(bias, residual, nullptr, nullptr, nullptr, "linear_norm_quant")) return status;
+    if (int status = check_norm(residual, gain, q, scale, N, "linear_norm_quant")) return status;
+    if (M == 0) return CHESS_OK;
+    Epilogue e{nullptr, nullptr, (const half_t*)bias, (const half_t*)residual, nullptr, nullptr, nullptr, 0,
+               (const half_t*)gain, (int8_t*)q, (float*)scale, eps};
+    hipStream_t s = (hipStream_t)stream;
+    if (bias) return launch_normalised<half_t, EPI_BIAS | EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
+    return launch_normalised<half_t, EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
+}
+
+extern "C" int chess_int8_linear_norm_quant(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* residual,
+                                            const void* original, const void* residual_scale, const void* input_scale, const void* gain,
+                                            void* out, void* q, void* scale, int M, int N, int K, float eps, void* stream)
+{
+    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES, 0, "int8_linear_norm_quant")) return status;
+    if (int status = check_epilogue(nullptr, residual, original, residual_scale, input_scale, "int8_linear_norm_quant")) return status;
+    if (int status = check_norm(residual, gain, q, scale, N, "int8_linear_norm_quant")) return status;
+    if (!x_scale || !w_scale) return chess_fail(CHESS_INVALID_SHAPE, "int8_linear_norm_quant needs both scales");
+    if (!aligned16(w_scale)) return chess_fail(CHESS_MISALIGNED, "int8_linear_norm_quant reads the weight scales 4 at a time");
+    if (M == 0) return CHESS_OK;
+    Epilogue e{(const float*)x_scale, (const float*)w_scale, nullptr, (const half_t*)residual, (const half_t*)original,
+               (const half_t*)residual_scale, (const half_t*)input_scale, 0, (const half_t*)gain, (int8_t*)q, (float*)scale, eps};
+    hipStream_t s = (hipStream_t)stream;
+    if (original) return launch_normalised<int8_t, EPI_RESIDUAL | EPI_MIX | EPI_NORM>(x, w, out, e, M, N, K, s);
+    return launch_normalised<int8_t, EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
 }

@@ -71,11 +71,21 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_template_attention(16, 8, 16, 16, 16, 1, 70, 8, 8, 64, 64, 8, 1, 1e-5, 0.125, None) == hip_kernels.MISALIGNED
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
+    # the normalising GEMMs: rows of 512 only, residual and the norm's operands required, 16-byte aligned gain and q
+    assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 4, 256, 64, 1e-5, None) == hip_kernels.UNSUPPORTED
+    assert b"512" in library.chess_last_error()
+    assert library.chess_linear_norm_quant(16, 16, None, None, 16, 16, 16, 16, 4, 512, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_linear_norm_quant(16, 16, None, 16, MISALIGNED, 16, 16, 16, 4, 512, 64, 1e-5, None) == hip_kernels.MISALIGNED
+    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 4, 512, 100, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, 16, None, None, 16, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, None, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
 
 
 def test_empty_batches_launch_nothing(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
+    assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 0, 512, 64, 1e-5, None) == 0
+    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 0, 512, 128, 1e-5, None) == 0
 
 
 def test_codes_become_value_errors_with_the_message(library):
