@@ -86,10 +86,9 @@ DEVICE float wave_max(float v) {
     return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
 }
 
-// One row of norm_quant's declared order on a wavefront, C contiguous elements a lane (zeros past the row's D):
-// the lane's squares as a pairwise tree, the wavefront's balanced tree (wave_sum), y = (v * (1 / sqrt(total / D + eps)))
-// * gain, absmax = max(max |y|, 1e-20), q = rint(y * (127 / absmax)). Returns absmax (the row's scale is absmax / 127).
-template <int C> DEVICE float norm_quant_row(const float (&v)[C], const float (&gain)[C], int D, float eps, int8_t (&q)[C]) {
+// The RMS norm's factor of one row on a wavefront, C contiguous elements a lane (zeros past the row's D): the lane's
+// squares as a pairwise tree, the wavefront's balanced tree (wave_sum), then 1 / sqrt(total / D + eps).
+template <int C> DEVICE float rms_inverse(const float (&v)[C], int D, float eps) {
     float squares[C];
 #pragma unroll
     for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
@@ -98,7 +97,13 @@ template <int C> DEVICE float norm_quant_row(const float (&v)[C], const float (&
 #pragma unroll
         for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
     const float total = wave_sum(squares[0]);
-    const float inverse = 1.0f / __builtin_sqrtf(total / (float)D + eps);
+    return 1.0f / __builtin_sqrtf(total / (float)D + eps);
+}
+
+// One row of norm_quant's declared order on a wavefront (C elements a lane, as rms_inverse): y = (v * inverse) * gain,
+// absmax = max(max |y|, 1e-20), q = rint(y * (127 / absmax)). Returns absmax (the row's scale is absmax / 127).
+template <int C> DEVICE float norm_quant_row(const float (&v)[C], const float (&gain)[C], int D, float eps, int8_t (&q)[C]) {
+    const float inverse = rms_inverse<C>(v, D, eps);
     float y[C];
     float largest = 0.0f;
 #pragma unroll

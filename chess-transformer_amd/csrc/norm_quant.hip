@@ -3,6 +3,8 @@
 //   [mixed = f16((x * rs) + (original * is))]
 //   y = (x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain
 //   absmax = max(max |y|, 1e-20);  q = rint(y * (127 / absmax));  scale = absmax / 127
+// Without the quantisation (QUANT false) the same kernel is the fp16 blocks' RMSNorm: out = f16(y), after the same
+// optional mix (model/fused_blocks.py:346-348 and :351, and the final norm at :863).
 // A wavefront takes R rows, one at a time, after loading all of them; a lane holds C = next_pow2(D) / 64
 // contiguous elements of a row (at least 1), sums its squares as a pairwise tree and the wavefront adds
 // the lanes' sums as a balanced tree of adjacent lanes, which is the balanced tree over the zero-padded row.
@@ -49,11 +51,11 @@ template <int C> DEVICE void widen(const half_t (&raw)[C], int col, int D, float
     for (int i = 0; i < C; i++) out[i] = col + i < D ? (float)raw[i] : 0.0f;
 }
 
-template <int C, int R, bool VECTOR>
+template <int C, int R, bool VECTOR, bool QUANT>
 __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
     const half_t* __restrict__ x, const half_t* __restrict__ original, const half_t* __restrict__ residual_scale,
     const half_t* __restrict__ input_scale, const half_t* __restrict__ gain, half_t* __restrict__ mixed,
-    int8_t* __restrict__ q, float* __restrict__ scale, int M, int D, float eps, int mix)
+    int8_t* __restrict__ q, float* __restrict__ scale, half_t* __restrict__ normed, int M, int D, float eps, int mix)
 {
     const int lane = threadIdx.x & 63;
     const int first = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
@@ -104,22 +106,40 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
             }
         }
 
-        int8_t out[C];
-        const float absmax = norm_quant_row<C>(v, g, D, eps, out);
-        if (vector) {
-            if (col < D) copy_bytes<C>(q + base + col, out);
-        } else {
+        if constexpr (QUANT) {
+            int8_t out[C];
+            const float absmax = norm_quant_row<C>(v, g, D, eps, out);
+            if (vector) {
+                if (col < D) copy_bytes<C>(q + base + col, out);
+            } else {
 #pragma unroll
-            for (int i = 0; i < C; i++)
-                if (col + i < D) q[base + col + i] = out[i];
+                for (int i = 0; i < C; i++)
+                    if (col + i < D) q[base + col + i] = out[i];
+            }
+            if (lane == 0) scale[row] = absmax / 127.0f;
+        } else {
+            const float inverse = rms_inverse<C>(v, D, eps);
+            half_t out[C];
+#pragma unroll
+            for (int i = 0; i < C; i++) {
+                float y = (v[i] * inverse) * g[i];
+                asm volatile("" : "+v"(y));   // the f32 product rounds to fp16 (one rounding of y, not a mixed multiply)
+                out[i] = (half_t)y;
+            }
+            if (vector) {
+                if (col < D) copy_bytes<2 * C>(normed + base + col, out);
+            } else {
+#pragma unroll
+                for (int i = 0; i < C; i++)
+                    if (col + i < D) normed[base + col + i] = out[i];
+            }
         }
-        if (lane == 0) scale[row] = absmax / 127.0f;
     }
 }
 
-template <int C>
+template <int C, bool QUANT>
 int launch(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
-           void* q, void* scale, int M, int D, float eps, hipStream_t stream)
+           void* q, void* scale, void* normed, int M, int D, float eps, hipStream_t stream)
 {
     // rows a wavefront: enough loads in flight to stream at HBM speed once the launch fills the chip, one row a
     // wavefront while it does not
@@ -127,12 +147,41 @@ int launch(const void* x, const void* original, const void* residual_scale, cons
     const bool wide = M >= 32768;
     const int rows_per_block = WAVES * (wide ? WIDE : 1);
     const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);
-    auto kernel = wide ? (D % C == 0 ? norm_quant_kernel<C, WIDE, true> : norm_quant_kernel<C, WIDE, false>)
-                       : (D % C == 0 ? norm_quant_kernel<C, 1, true> : norm_quant_kernel<C, 1, false>);
+    auto kernel = wide ? (D % C == 0 ? norm_quant_kernel<C, WIDE, true, QUANT> : norm_quant_kernel<C, WIDE, false, QUANT>)
+                       : (D % C == 0 ? norm_quant_kernel<C, 1, true, QUANT> : norm_quant_kernel<C, 1, false, QUANT>);
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, (const half_t*)x, (const half_t*)original, (const half_t*)residual_scale,
-                       (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q, (float*)scale, M, D, eps,
-                       original != nullptr ? 1 : 0);
+                       (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q, (float*)scale, (half_t*)normed, M, D,
+                       eps, original != nullptr ? 1 : 0);
     return launch_status();
+}
+
+template <bool QUANT>
+int by_width(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed, void* q,
+             void* scale, void* normed, int M, int D, float eps, hipStream_t s)
+{
+    int padded = 64;
+    while (padded < D) padded <<= 1;
+    switch (padded / 64) {
+        case 1: return launch<1, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 2: return launch<2, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 4: return launch<4, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 8: return launch<8, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 16: return launch<16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        default: return launch<32, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+    }
+}
+
+int check_rows(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
+               int M, int D, const char* what)
+{
+    if (M < 0 || D <= 0) return chess_fail(CHESS_INVALID_SHAPE, "%s: rows %d and width %d", what, M, D);
+    if (D > 64 * 32) return chess_fail(CHESS_UNSUPPORTED, "%s takes rows of at most 2048, not %d", what, D);
+    if (!x || !gain) return chess_fail(CHESS_INVALID_SHAPE, "%s: a required pointer is null", what);
+    if (original && (!residual_scale || !input_scale || !mixed))
+        return chess_fail(CHESS_INVALID_SHAPE, "%s's input mix needs the scales and the mixed output", what);
+    if (!aligned16(x) || (original && (!aligned16(original) || !aligned16(mixed))))
+        return chess_fail(CHESS_MISALIGNED, "%s's vector loads need 16-byte aligned rows", what);
+    return CHESS_OK;
 }
 
 }  // namespace
@@ -140,23 +189,19 @@ int launch(const void* x, const void* original, const void* residual_scale, cons
 extern "C" int chess_norm_quant(const void* x, const void* original, const void* residual_scale, const void* input_scale,
                                 const void* gain, void* mixed, void* q, void* scale, int M, int D, float eps, void* stream)
 {
-    if (M < 0 || D <= 0) return chess_fail(CHESS_INVALID_SHAPE, "norm_quant: rows %d and width %d", M, D);
-    if (D > 64 * 32) return chess_fail(CHESS_UNSUPPORTED, "norm_quant takes rows of at most 2048, not %d", D);
-    if (!x || !gain || !q || !scale) return chess_fail(CHESS_INVALID_SHAPE, "norm_quant: a required pointer is null");
-    if (original && (!residual_scale || !input_scale || !mixed))
-        return chess_fail(CHESS_INVALID_SHAPE, "mix_norm_quant needs the scales and the mixed output");
-    if (!aligned16(x) || !aligned16(q) || (original && (!aligned16(original) || !aligned16(mixed))))
-        return chess_fail(CHESS_MISALIGNED, "norm_quant's vector loads need 16-byte aligned rows");
+    if (int status = check_rows(x, original, residual_scale, input_scale, gain, mixed, M, D, "norm_quant")) return status;
+    if (!q || !scale) return chess_fail(CHESS_INVALID_SHAPE, "norm_quant: a required pointer is null");
+    if (!aligned16(q)) return chess_fail(CHESS_MISALIGNED, "norm_quant's vector loads need 16-byte aligned rows");
     if (M == 0) return CHESS_OK;
-    int padded = 64;
-    while (padded < D) padded <<= 1;
-    hipStream_t s = (hipStream_t)stream;
-    switch (padded / 64) {
-        case 1: return launch<1>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-        case 2: return launch<2>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-        case 4: return launch<4>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-        case 8: return launch<8>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-        case 16: return launch<16>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-        default: return launch<32>(x, original, residual_scale, input_scale, gain, mixed, q, scale, M, D, eps, s);
-    }
+    return by_width<true>(x, original, residual_scale, input_scale, gain, mixed, q, scale, nullptr, M, D, eps, (hipStream_t)stream);
+}
+
+extern "C" int chess_rms_norm(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain,
+                              void* mixed, void* out, int M, int D, float eps, void* stream)
+{
+    if (int status = check_rows(x, original, residual_scale, input_scale, gain, mixed, M, D, "rms_norm")) return status;
+    if (!out) return chess_fail(CHESS_INVALID_SHAPE, "rms_norm: a required pointer is null");
+    if (!aligned16(out)) return chess_fail(CHESS_MISALIGNED, "rms_norm's vector loads need 16-byte aligned rows");
+    if (M == 0) return CHESS_OK;
+    return by_width<false>(x, original, residual_scale, input_scale, gain, mixed, nullptr, nullptr, out, M, D, eps, (hipStream_t)stream);
 }

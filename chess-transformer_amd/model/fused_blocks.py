@@ -175,6 +175,55 @@ def _(x, weight, bias=None, residual=None, gated=False, accumulate_fp32=False, o
     return x.new_empty(*x.shape[:-1], weight.shape[1] // 2 if gated else weight.shape[1], dtype=torch.float32 if accumulate_fp32 else x.dtype)
 
 
+def launch_rms_norm(x: torch.Tensor, original: torch.Tensor | None, residual_scale: torch.Tensor | None, input_scale: torch.Tensor | None,
+                    gain: torch.Tensor, eps: float) -> tuple[torch.Tensor | None, torch.Tensor]:
+    """(mixed or None, f16(RMSNorm(mixed or x) * gain)): the fp16 blocks' norms in norm_quant's f32 order, one launch."""
+    for tensor, name in ((x, "x"), (original, "original"), (residual_scale, "residual_scale"), (input_scale, "input_scale"), (gain, "gain")):
+        if tensor is not None and tensor.dtype != torch.float16:
+            raise ValueError(f"rms_norm's {name} is {tensor.dtype}, the kernel takes fp16")
+    library = library_for(x.device)
+    x, original = aligned(x), aligned(original)
+    D = x.shape[-1]
+    if gain.numel() != D:
+        raise ValueError(f"rms_norm: {gain.numel()} gains for rows of {D}")
+    if original is not None and original.shape != x.shape:
+        raise ValueError(f"rms_norm: the input {tuple(original.shape)} does not match the stream {tuple(x.shape)}")
+    mixed = torch.empty_like(x) if original is not None else None
+    out = torch.empty_like(x)
+    code = library.chess_rms_norm(pointer(x), pointer(original), pointer(residual_scale), pointer(input_scale), pointer(gain.contiguous()),
+                                  pointer(mixed), pointer(out), x.numel() // D, D, float(eps), stream_of(x.device))
+    check(code, "rms_norm")
+    return mixed, out
+
+
+def norm_eps(norm: nn.RMSNorm, x: torch.Tensor) -> float:
+    """nn.RMSNorm's eps: its own, or the dtype's machine epsilon when it has none (as torch's rms_norm takes it)."""
+    return norm.eps if norm.eps is not None else torch.finfo(x.dtype).eps
+
+
+#the fp16 blocks' RMSNorm (nn.RMSNorm at reference fused_blocks.py:348, 351, 863), f32 inside, fp16 out
+@torch.library.custom_op("chess::rms_norm", mutates_args=())
+def rms_norm(x: torch.Tensor, gain: torch.Tensor, eps: float) -> torch.Tensor:
+    return launch_rms_norm(x, None, None, None, gain, eps)[1]
+
+
+@rms_norm.register_fake
+def _(x, gain, eps):
+    return torch.empty_like(x)
+
+
+#the fp16 block's own input mix and its ln1 (reference fused_blocks.py:346-348): (mixed, normalised)
+@torch.library.custom_op("chess::mix_rms_norm", mutates_args=())
+def mix_rms_norm(x: torch.Tensor, original: torch.Tensor, residual_scale: torch.Tensor, input_scale: torch.Tensor, gain: torch.Tensor,
+                 eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    return launch_rms_norm(x, original, residual_scale, input_scale, gain, eps)
+
+
+@mix_rms_norm.register_fake
+def _(x, original, residual_scale, input_scale, gain, eps):
+    return torch.empty_like(x), torch.empty_like(x)
+
+
 def transposed(weight: torch.Tensor) -> nn.Parameter:
     return nn.Parameter(weight.detach().t().contiguous())
 
@@ -203,12 +252,15 @@ class FusedBlock(nn.Module):
         self.input_mixed = False
 
     def forward(self, x: torch.Tensor, templates: torch.Tensor, original_board_embed: torch.Tensor) -> torch.Tensor:
-        if not self.input_mixed:
-            x = self.residual_scale * x + self.input_scale * original_board_embed
-        attended = template_attention(linear(self.ln1(x), self.projection, self.projection_bias), templates, self.q_gain, self.k_gain, self.heads,
+        #the input mix, when this block makes it, is (x * rs) + (original * is) rounded once, as the int8 blocks' mix
+        if self.input_mixed:
+            normed = rms_norm(x, self.ln1.weight, norm_eps(self.ln1, x))
+        else:
+            x, normed = mix_rms_norm(x, original_board_embed, self.residual_scale, self.input_scale, self.ln1.weight, norm_eps(self.ln1, x))
+        attended = template_attention(linear(normed, self.projection, self.projection_bias), templates, self.q_gain, self.k_gain, self.heads,
                                       self.kv_heads, self.dq, self.dv, self.templates_count, self.eps)
         x = linear(attended, self.combine_heads, self.combine_heads_bias, residual=x)
-        hidden = linear(self.ln2(x), self.gate_up, gated=True)
+        hidden = linear(rms_norm(x, self.ln2.weight, norm_eps(self.ln2, x)), self.gate_up, gated=True)
         if self.next_scales is None:
             return linear(hidden, self.down, residual=x)
         return linear(hidden, self.down, residual=x, original=original_board_embed, residual_scale=self.next_scales[0], input_scale=self.next_scales[1])
@@ -314,7 +366,7 @@ class FusedTransformer(nn.Module):
         original_board_embed = embed_state
         for block in self.encoder:
             embed_state = block(embed_state, self.templates, original_board_embed)
-        model_output = self.ln(embed_state)
+        model_output = rms_norm(embed_state, self.ln.weight, norm_eps(self.ln, embed_state))
 
         with torch.autocast(device_type=board_state.device.type, enabled=False):
             #the f32 bias after the kernel, which takes fp16 biases

@@ -31,6 +31,13 @@ extern "C" {
 int chess_norm_quant(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain,
                      void* mixed, void* q, void* scale, int M, int D, float eps, void* stream);
 
+/* The fp16 blocks' RMSNorm: out[M, D] = f16((x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain), the f32 order of
+ * chess_norm_quant without its quantisation; with original, x is first mixed as there (mixed = f16((x * residual_scale)
+ * + (original * input_scale)), written to mixed) and the mixed rows are normalised. Replaces the fp16 block's input mix
+ * and ln1 (model/fused_blocks.py:346-348), its ln2 (:351) and the network's final norm (:863), torch's nn.RMSNorm. */
+int chess_rms_norm(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
+                   void* out, int M, int D, float eps, void* stream);
+
 /* h[M, N] fp16 zero-padded to width, each 32-column block times Sylvester's H32, then per-row int8:
  * q[M, width], scale[M]. Replaces model/int8_blocks.py:216-246 (rotate_quant_kernel, op rotate_quant). */
 int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int width, void* stream);

@@ -109,6 +109,16 @@ def mix_norm_quant(x, original, residual_scale, input_scale, gain, eps) -> tuple
     return mixed, q, scale
 
 
+def rms_norm(x: np.ndarray, gain: np.ndarray, eps: float, original=None, residual_scale=None, input_scale=None):
+    """The fp16 blocks' RMSNorm (nn.RMSNorm in fp16 at model/fused_blocks.py:348, 351 and 863), in norm_quant's f32 order
+    rounded once to fp16: (mixed or None, f16(rms_normalise(mixed or x))). With original, the block's own input mix
+    (:346-347) comes first, as mix() rounds it."""
+    mixed = mix(x, original, residual_scale, input_scale) if original is not None else None
+    rows = mixed if mixed is not None else x
+    normed = rms_normalise(rows.reshape(-1, rows.shape[-1]), gain, eps).astype(F16)
+    return mixed, normed.reshape(rows.shape)
+
+
 def fwht32(rows: np.ndarray) -> np.ndarray:
     """rows[..., 32] @ hadamard(32) as five f32 butterfly stages, spans 1, 2, 4, 8, 16: (a, b) -> (a + b, a - b)."""
     out = rows.astype(F32)

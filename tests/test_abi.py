@@ -54,6 +54,10 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, -1, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE
     assert b"rows" in library.chess_last_error()
     assert library.chess_norm_quant(MISALIGNED, None, None, None, 16, None, 16, 16, 4, 64, 1e-5, None) == hip_kernels.MISALIGNED
+    assert library.chess_rms_norm(16, None, None, None, 16, None, 16, -1, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_rms_norm(16, None, None, None, 16, None, 16, 4, 4096, 1e-5, None) == hip_kernels.UNSUPPORTED
+    assert library.chess_rms_norm(16, 16, None, None, 16, None, 16, 4, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE   # a mix without scales
+    assert library.chess_rms_norm(16, None, None, None, 16, None, MISALIGNED, 4, 64, 1e-5, None) == hip_kernels.MISALIGNED
     assert library.chess_rotate_quant(16, 16, 16, 4, 100, 100, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 4, 8, 100, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert b"64 at a time" in library.chess_last_error()
@@ -83,6 +87,7 @@ def test_refused_shapes_come_back_as_codes(library):
 
 def test_empty_batches_launch_nothing(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
+    assert library.chess_rms_norm(16, None, None, None, 16, None, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
     assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 0, 512, 64, 1e-5, None) == 0
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 0, 512, 128, 1e-5, None) == 0

@@ -15,7 +15,7 @@ from oracle import int8_ops as oracle
 from model import fused_blocks, int8_blocks
 from model.int8_blocks import (HADAMARD_BLOCK, INT8_TILES, hadamard, int8_linear, int8_linear_norm_quant, int8_matmul_i32, launch_int8_linear,
                                linear_norm_quant, mix_norm_quant, norm_quant, rotate_quant)
-from model.fused_blocks import launch_linear, launch_template_attention, linear, template_attention
+from model.fused_blocks import launch_linear, launch_template_attention, linear, mix_rms_norm, rms_norm, template_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -46,6 +46,30 @@ def test_norm_quant_matches_the_oracle_to_the_bit(device, D, mix):
         expected_q, expected_scale = oracle.norm_quant(cpu(x), cpu(gain), 1e-5)
     assert q.dtype == torch.int8 and scale.dtype == torch.float32
     assert bits_equal(q, expected_q) and bits_equal(scale, expected_scale)
+
+
+@pytest.mark.parametrize("rows, D", [(210, 128), (210, 192), (210, 512), (210, 768), (40000, 512)])
+@pytest.mark.parametrize("mix", [False, True])
+def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
+    """The fp16 blocks' norm (and their own input mix): the oracle's bits, one and four rows a wavefront (40,000 rows);
+    within one fp16 rounding of torch's rms_norm in f32 (the reference's nn.RMSNorm)."""
+    torch.manual_seed(rows + D)
+    x = (torch.randn(rows, D, device=device) * 4).half()
+    original = torch.randn(rows, D, device=device).half()
+    gain = (torch.rand(D, device=device) + 0.5).half()
+    rs, is_ = torch.tensor([0.8], device=device).half(), torch.tensor([0.5], device=device).half()
+    if mix:
+        mixed, normed = mix_rms_norm(x, original, rs, is_, gain, 1e-5)
+        expected_mixed, expected = oracle.rms_norm(cpu(x), cpu(gain), 1e-5, cpu(original), cpu(rs), cpu(is_))
+        assert bits_equal(mixed, expected_mixed)
+        rows_in = mixed
+    else:
+        normed = rms_norm(x, gain, 1e-5)
+        expected = oracle.rms_norm(cpu(x), cpu(gain), 1e-5)[1]
+        rows_in = x
+    assert normed.dtype == torch.float16 and bits_equal(normed, expected)
+    torchs = F.rms_norm(rows_in.float(), (D,), gain.float(), 1e-5)
+    assert ((normed.float() - torchs).abs() <= torchs.half().abs().float() * 2 ** -10 + 2 ** -24).all()
 
 
 def test_norm_quant_rounds_the_rmsnorm(device):

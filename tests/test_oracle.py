@@ -49,6 +49,24 @@ def test_norm_quant_rounds_the_rmsnorm(D):
     assert (np.abs(q * scale[:, None].astype(np.float64) - normed) <= 0.501 * step[:, None]).all()
 
 
+@pytest.mark.parametrize("D", [64, 96, 512])
+def test_rms_norm_is_torchs_to_an_fp16_step(D):
+    """The fp16 blocks' norm against torch's rms_norm in float64 (the reference's nn.RMSNorm): within one rounding of fp16,
+    so a dropped eps, a wrong width or a missing gain fails; with the mix, it is the mix then the norm."""
+    x = (RNG.standard_normal((40, D)) * 4).astype(np.float16)
+    x[0] = 0
+    gain = (RNG.random(D) + 0.5).astype(np.float16)
+    mixed, normed = oracle.rms_norm(x, gain, 1e-2)
+    expected = F.rms_norm(torch.from_numpy(x).double(), (D,), torch.from_numpy(gain).double(), 1e-2).numpy()
+    assert mixed is None and normed.dtype == np.float16 and (normed[0] == 0).all()
+    assert (np.abs(normed.astype(np.float64) - expected) <= np.spacing(np.abs(expected).astype(np.float16)).astype(np.float64)).all()
+    original = RNG.standard_normal((40, D)).astype(np.float16)
+    rs, is_ = np.float16(0.8), np.float16(0.5)
+    mixed, normed = oracle.rms_norm(x, gain, 1e-2, original, rs, is_)
+    assert np.array_equal(mixed, oracle.mix(x, original, rs, is_))
+    assert np.array_equal(normed, oracle.rms_norm(mixed, gain, 1e-2)[1])
+
+
 def test_a_zero_row_quantises_to_zero():
     q, scale = oracle.norm_quant(np.zeros((2, 64), np.float16), np.ones(64, np.float16), 1e-5)
     assert (q == 0).all() and np.allclose(scale, 1e-20 / 127)
