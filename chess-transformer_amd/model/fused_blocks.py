@@ -330,6 +330,47 @@ class InputEmbedding(nn.Module):
 
 
 #logits[i, j] = (W_f x_i + b_f) . (W_t x_j + b_t) / sqrt(d) = a_i . x_j + s_i: from and to as one d x d matmul (a)
+#the policy head's move logits after its `a` matmul and board_down's inputs (reference fused_blocks.py:866-871), one launch
+@torch.library.custom_op("chess::move_logits", mutates_args=())
+def move_logits(x: torch.Tensor, a: torch.Tensor, a_bias: torch.Tensor, narrow_weight: torch.Tensor, narrow_bias: torch.Tensor, cells: torch.Tensor,
+                promotions: torch.Tensor, down_first: int) -> tuple[torch.Tensor, torch.Tensor]:
+    B, T, D = x.shape
+    for tensor, dtype, name in ((x, torch.float16, "x"), (a, torch.float32, "a"), (a_bias, torch.float32, "a_bias"),
+                                (narrow_weight, torch.float32, "narrow_weight"), (narrow_bias, torch.float32, "narrow_bias"),
+                                (cells, torch.int32, "cells"), (promotions, torch.int32, "promotions")):
+        if tensor.dtype != dtype:
+            raise ValueError(f"move_logits' {name} is {tensor.dtype}, the kernel takes {dtype}")
+    if a.shape != x.shape or a_bias.numel() != D or narrow_weight.shape[1] != D or narrow_bias.numel() != narrow_weight.shape[0]:
+        raise ValueError(f"move_logits: x {tuple(x.shape)}, a {tuple(a.shape)}, a_bias {a_bias.numel()}, narrow {tuple(narrow_weight.shape)}")
+    if cells.shape != promotions.shape:
+        raise ValueError("move_logits: a cell and a promotion place for every move")
+    library = library_for(x.device)
+    x, a, a_bias, narrow_weight = aligned(x), aligned(a), aligned(a_bias), aligned(narrow_weight)
+    narrow = narrow_weight.shape[0]
+    out = torch.empty(B, cells.numel(), device=x.device, dtype=torch.float32)
+    down = torch.empty(B, T, narrow - down_first, device=x.device, dtype=torch.float32)
+    code = library.chess_move_logits(pointer(x), pointer(a), pointer(a_bias), pointer(narrow_weight), pointer(narrow_bias.contiguous()),
+                                     pointer(cells.contiguous()), pointer(promotions.contiguous()), pointer(out), pointer(down), B, T, D, narrow,
+                                     down_first, cells.numel(), stream_of(x.device))
+    check(code, "move_logits")
+    return out, down
+
+
+@move_logits.register_fake
+def _(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first):
+    B, T, _ = x.shape
+    return x.new_empty(B, cells.numel(), dtype=torch.float32), x.new_empty(B, T, narrow_weight.shape[0] - down_first, dtype=torch.float32)
+
+
+def move_places(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per move, from * 64 + to and the place of its promotion logit among the narrow columns, to' * 32 + 1 + piece (-1 for none):
+    the gathers of reference fused_blocks.py:869-870 as two int32 tables."""
+    cells = (model.from_squares * NUM_SQUARES + model.to_squares).int()
+    promotions = torch.full_like(cells, -1)
+    promotions[model.promotion_move_ids] = (model.promotion_to_squares * 32 + 1 + model.promotion_pieces).int()
+    return cells, promotions
+
+
 def head_weights(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
     with torch.no_grad():
         from_weight, from_bias = model.from_projection.weight.double(), model.from_projection.bias.double()
@@ -360,6 +401,9 @@ class FusedTransformer(nn.Module):
         self.a_weight, self.a_bias, self.narrow_weight, self.narrow_bias = (nn.Parameter(tensor, requires_grad=False) for tensor in head_weights(model))
         promotions = model.promotion_projection.out_features
         self.promotion_columns, self.down_columns = slice(1, 1 + promotions), slice(1 + promotions, None)
+        cells, promotion_places = move_places(model)
+        self.register_buffer("move_cells", cells)
+        self.register_buffer("move_promotions", promotion_places)
 
     def forward(self, board_state: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         embed_state = self.input_embedding(board_state)
@@ -369,13 +413,10 @@ class FusedTransformer(nn.Module):
         model_output = rms_norm(embed_state, self.ln.weight, norm_eps(self.ln, embed_state))
 
         with torch.autocast(device_type=board_state.device.type, enabled=False):
-            #the f32 bias after the kernel, which takes fp16 biases
-            a = linear(model_output.half(), self.a_weight, accumulate_fp32=True) + self.a_bias
-            model_output = model_output.float()
-            narrow = F.linear(model_output, self.narrow_weight, self.narrow_bias)  #B T: s, the promotion logits, board_down_project's
-            squares = narrow[:, :NUM_SQUARES]
-            logits = a[:, :NUM_SQUARES] @ model_output[:, :NUM_SQUARES].transpose(1, 2).contiguous() + squares[..., :1]
-            combined_logits = logits[:, self.from_squares, self.to_squares]
-            combined_logits[:, self.promotion_move_ids] += squares[..., self.promotion_columns][:, self.promotion_to_squares, self.promotion_pieces]
-            compressed_board = self.board_down_activation(narrow[..., self.down_columns]).reshape(board_state.shape[0], -1)
+            #a = x @ a_weight in f32 sums; its f32 bias, the narrow products (s, the promotion logits, board_down_project's), the
+            #bilinear logits and the gathers of the moves are one launch
+            a = linear(model_output, self.a_weight, accumulate_fp32=True)
+            combined_logits, board_down = move_logits(model_output, a, self.a_bias, self.narrow_weight, self.narrow_bias, self.move_cells,
+                                                      self.move_promotions, self.down_columns.start)
+            compressed_board = self.board_down_activation(board_down).reshape(board_state.shape[0], -1)
             return combined_logits, self.eval_head(compressed_board)

@@ -101,6 +101,16 @@ int chess_board_embedding(const void* boards, int code_bytes, const void* rays, 
                           const void* position, const void* table, void* out, int B, int T, int D, int embed_rows, int table_rows, int pawn,
                           int knight, int queen, int king, int theirs, int edge, int no_piece, void* stream);
 
+/* The policy head's move logits of B positions after its `a` matmul (model/fused_blocks.py:863-872, the heads without
+ * fused ends): x[B, T, D] the final norm's rows (fp16), a[B, T, D] = x @ a_weight (f32, rows 0..63 read), a_bias[D],
+ * w[NN, D] and w_bias[NN] the narrow projections (f32: s, the promotion logits, board_down's inputs from down_first),
+ * cells[moves] = from * 64 + to and promotions[moves] = to' * 32 + column of the move's promotion logit or -1 (int32).
+ * out[B, moves] f32 = ((a[from] + a_bias) . x[to]) + narrow[from][0] (+ narrow[to'][column]); down[B, T, NN - down_first]
+ * f32 = narrow[t][down_first..NN). 64 <= T <= 96, D % 64 == 0, NN <= 32. Replaces the torch ops of :866-871 (the f32
+ * linear, the transposed bmm, the gathers and the promotion sum). */
+int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
+                      const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves, void* stream);
+
 /* Fills table[0..6] with hipSetDevice, hipMemcpyAsync, hipGraphLaunch, hipEventRecord, hipEventSynchronize,
  * hipStreamSynchronize, hipGetErrorString: the address table of engine/cuda_runtime.py:17-49 (CudaRuntime.CALLS
  * and addresses()), whose HIP functions have the CUDA ones' signatures; the native round loop

@@ -75,6 +75,12 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_template_attention(16, 8, 16, 16, 16, 1, 70, 8, 8, 64, 64, 8, 1, 1e-5, 0.125, None) == hip_kernels.MISALIGNED
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
+    moves = lambda *shape: library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, *shape, None)
+    assert moves(2, 63, 512, 21, 5, 1968) == hip_kernels.UNSUPPORTED      # fewer tokens than squares
+    assert moves(2, 70, 500, 21, 5, 1968) == hip_kernels.UNSUPPORTED      # width not a multiple of 8
+    assert moves(2, 70, 512, 33, 5, 1968) == hip_kernels.INVALID_SHAPE    # more narrow columns than a block
+    assert moves(2, 70, 512, 21, 0, 1968) == hip_kernels.INVALID_SHAPE    # board_down's inputs from column 0
+    assert library.chess_move_logits(MISALIGNED, 16, 16, 16, 16, 16, 16, 16, 16, 2, 70, 512, 21, 5, 1968, None) == hip_kernels.MISALIGNED
     # the normalising GEMMs: rows of 512 only, residual and the norm's operands required, 16-byte aligned gain and q
     assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 4, 256, 64, 1e-5, None) == hip_kernels.UNSUPPORTED
     assert b"512" in library.chess_last_error()
@@ -88,6 +94,7 @@ def test_refused_shapes_come_back_as_codes(library):
 def test_empty_batches_launch_nothing(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_rms_norm(16, None, None, None, 16, None, 16, 0, 64, 1e-5, None) == 0
+    assert library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, 0, 70, 512, 21, 5, 1968, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
     assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 0, 512, 64, 1e-5, None) == 0
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 0, 512, 128, 1e-5, None) == 0

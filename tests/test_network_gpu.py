@@ -142,6 +142,30 @@ def test_the_normalising_gemms_change_no_answer(device, monkeypatch):
     assert torch.equal(fused, separate)
 
 
+@pytest.mark.parametrize("settings", [SMALL, FULL])
+def test_the_move_logits_are_the_heads_torch_ops(device, settings):
+    """The policy head's launch against the torch ops it replaces (reference fused_blocks.py:866-871), in float64: the
+    bilinear logits gathered to the moves with the promotion logits added, and board_down's inputs."""
+    model = make_model(settings, seed=11)
+    fused = fused_blocks.FusedTransformer(copy.deepcopy(model).scale_residual_stream(FP16_RESIDUAL_SCALE).half_except_heads(torch.float16)).to(device)
+    torch.manual_seed(11)
+    B, T, D = 6, 70, settings["d_model"]
+    x = torch.randn(B, T, D, device=device).half()
+    with torch.no_grad():
+        a = linear(x, fused.a_weight, accumulate_fp32=True)
+        logits, down = fused_blocks.move_logits(x, a, fused.a_bias, fused.narrow_weight, fused.narrow_bias, fused.move_cells,
+                                                fused.move_promotions, fused.down_columns.start)
+        xd, ad = x.double(), a.double() + fused.a_bias.double()
+        narrow = xd @ fused.narrow_weight.double().T + fused.narrow_bias.double()
+        expected = ad[:, :64] @ xd[:, :64].transpose(1, 2).contiguous() + narrow[:, :64, :1]
+        expected = expected[:, fused.from_squares, fused.to_squares]
+        squares = narrow[:, :64]
+        expected[:, fused.promotion_move_ids] += squares[..., fused.promotion_columns][:, fused.promotion_to_squares, fused.promotion_pieces]
+    assert logits.shape == (B, len(fused.from_squares)) and down.shape == (B, T, narrow.shape[-1] - fused.down_columns.start)
+    assert torch.allclose(logits.double(), expected, atol=1e-4, rtol=1e-4)
+    assert torch.allclose(down.double(), narrow[..., fused.down_columns], atol=1e-4, rtol=1e-4)
+
+
 def test_tiles_change_no_answer(device, monkeypatch):
     network = int8_network(make_model().to(device), nearest_int8_weights(make_model()))
     with torch.no_grad():
