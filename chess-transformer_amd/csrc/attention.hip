@@ -9,8 +9,8 @@
 // templates for 4 keys as 4 16-byte loads (the reference pairs its templates likewise,
 // model/attention_cuda.py:410-440).
 //
-// A workgroup takes one position and one or more key/value groups; it has one wavefront per slab of
-// 16 queries. For each group the workgroup stages the normalised keys [key][dq] and the values,
+// A workgroup takes a run of groups_per_block (position, key/value group) pairs, in order, which may run on
+// from one position into the next; it has one wavefront per slab of 16 queries. For each group the workgroup stages the normalised keys [key][dq] and the values,
 // transposed, [d][key] in LDS. A wavefront then runs each head of the group on v_mfma_f32_16x16x32_f16:
 // the scores come out transposed, S^T = K Q^T, so a lane holds one query's scores for 4 keys of each
 // 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B operand, so the probabilities
@@ -135,11 +135,12 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int b = blockIdx.y;
     const int width = heads * dq + kv_heads * dq + kv_heads * DV + heads * templates_count;
     const int k_offset = heads * dq, v_offset = k_offset + kv_heads * dq, c_offset = v_offset + kv_heads * DV;
     const int per_kv = heads / kv_heads;
-    const half_t* board = projected + (size_t)b * T * width;
+    // pair p of the launch is key/value group p % kv_heads of position p / kv_heads
+    auto board_of = [&](int pair) { return projected + (size_t)(pair / kv_heads) * T * width; };
+    const int first_pair = blockIdx.x * groups_per_block;
     const int head_bytes = L::RAW_Q_BYTES;
 
     const int col = lane & 15, quad = lane >> 4;
@@ -154,8 +155,10 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     value_plan.plan(T - 1, width, slab, lane);
     const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
 
-    // a group's keys, queries and coefficients (into a buffer), or its values
-    auto dma_group = [&](int group, bool v, bool kq, int buffer) {
+    // a pair's keys, queries and coefficients (into a buffer), or its values
+    auto dma_group = [&](int pair, bool v, bool kq, int buffer) {
+        const half_t* board = board_of(pair);
+        const int group = pair % kv_heads;
         if (v) value_plan.issue(raw_v, board + v_offset + group * DV, slab);
         if (kq) {
             key_plan.issue(raw_k + buffer * L::RAW_K_BYTES, board + k_offset + group * dq, slab);
@@ -168,7 +171,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             }
         }
     };
-    dma_group(blockIdx.x * groups_per_block, true, true, 0);
+    dma_group(first_pair, true, true, 0);
 
     // The template bias of a 16-key tile is an MFMA too: bias^T[k][q] = sum over (q', t) of templates[t][q'][k] *
     // [q' == q] c[q][t], an inner dimension of the wavefront's 16 queries x 8 templates, 32 a step. In step j the A
@@ -217,10 +220,10 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     // starts -- 16 bytes a lane along the rows, where the wait at the start of the group after finds them long done.
     // Stored straight from the MFMA layout, 8 bytes a lane scattered over 16 rows, they would be waited for at once.
     constexpr bool STAGED = DV <= DQP;
-    auto write_out = [&](int group, int buffer) {
+    auto write_out = [&](int pair, int buffer) {
         for (int hi = 0; hi < per_kv; hi++) {
             const LDS_SPACE int8_t* staged = raw_q + (buffer * per_kv + hi) * head_bytes;
-            half_t* to = out + (size_t)b * T * (heads * DV) + (group * per_kv + hi) * DV;
+            half_t* to = out + (size_t)(pair / kv_heads) * T * (heads * DV) + (pair % kv_heads * per_kv + hi) * DV;
 #pragma unroll
             for (int k = 0; k < O_ITEMS; k++) {
                 const int item = tid + k * THREADS, q = item / VC, c = item % VC;
@@ -233,14 +236,16 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     };
 
     for (int gi = 0; gi < groups_per_block; gi++) {
-        const int group = blockIdx.x * groups_per_block + gi;
+        const int pair = first_pair + gi, group = pair % kv_heads;
+        const size_t b = pair / kv_heads;
+        const half_t* board = board_of(pair);
         const int buffer = gi & 1;
         // this group's raw rows have landed (this wavefront's DMA), and every wavefront is past the previous group
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
         // the previous group's outputs leave its query buffer before the next group's queries come into it
-        if (STAGED && gi > 0) write_out(group - 1, buffer ^ 1);
-        if (gi + 1 < groups_per_block) dma_group(group + 1, false, true, buffer ^ 1);
+        if (STAGED && gi > 0) write_out(pair - 1, buffer ^ 1);
+        if (gi + 1 < groups_per_block) dma_group(pair + 1, false, true, buffer ^ 1);
 
         // the keys' scales: scale * rsqrt(mean of squares + eps) over the key's dq columns. Past dq a raw key chunk
         // holds another head's columns: zeroed here, as a zero query column would not cancel an infinite one.
@@ -280,7 +285,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
         }
         lds_barrier();
         // the raw values are read: the next group's come in while this one's heads run
-        if (gi + 1 < groups_per_block) dma_group(group + 1, true, false, 0);
+        if (gi + 1 < groups_per_block) dma_group(pair + 1, true, false, 0);
 
         for (int hi = 0; hi < per_kv; hi++) {
             const int head = group * per_kv + hi;
@@ -416,7 +421,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                     lds_write8(row + raw_slot<KC>(query, 2 * dt + quad / 2) * 16 + (quad & 1) * 8, __builtin_bit_cast(uint2, result));
                 }
             } else if (query_ok) {
-                half_t* to = out + ((size_t)b * T + query) * (heads * DV) + head * DV + quad * 4;
+                half_t* to = out + (b * T + query) * (heads * DV) + head * DV + quad * 4;
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
                     const v4h result = v4h{(half_t)(o[dt][0] * inverse_total), (half_t)(o[dt][1] * inverse_total),
@@ -429,7 +434,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     if constexpr (STAGED) {
         __builtin_amdgcn_s_waitcnt(0);   // this wavefront's staging writes are done (the compiler does not see them)
         __syncthreads();
-        write_out(blockIdx.x * groups_per_block + groups_per_block - 1, (groups_per_block - 1) & 1);
+        write_out(first_pair + groups_per_block - 1, (groups_per_block - 1) & 1);
     }
 }
 
@@ -446,7 +451,7 @@ int launch(const void* projected, const void* keyed, const void* q_gain, const v
         const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (allowed != hipSuccess) return (int)allowed;
     }
-    const dim3 grid(kv_heads / groups_per_block, B), block(64 * TILES);   // TILES == ceil(T / 16): the caller picked it so
+    const dim3 grid((unsigned)((long)B * kv_heads / groups_per_block)), block(64 * TILES);   // TILES == ceil(T / 16): the caller picked it so
     hipLaunchKernelGGL(kernel, grid, block, bytes, stream, (const half_t*)projected, (const half_t*)keyed, (const half_t*)q_gain,
                        (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale);
     return launch_status();
@@ -491,8 +496,8 @@ extern "C" int chess_template_attention(const void* projected, const void* keyed
     if (dv != 16 && dv != 32 && dv != 64 && dv != 128) return chess_fail(CHESS_UNSUPPORTED, "template_attention takes value widths 16, 32, 64 or 128, not %d", dv);
     if (templates_count < 0 || templates_count > MAX_TEMPLATES)
         return chess_fail(CHESS_UNSUPPORTED, "template_attention takes at most %d templates, not %d", MAX_TEMPLATES, templates_count);
-    if (groups_per_block <= 0 || kv_heads % groups_per_block != 0)
-        return chess_fail(CHESS_INVALID_SHAPE, "%d key/value groups a workgroup do not divide %d", groups_per_block, kv_heads);
+    if (groups_per_block <= 0 || ((long)B * kv_heads) % groups_per_block != 0)
+        return chess_fail(CHESS_INVALID_SHAPE, "%d key/value groups a workgroup do not divide the %d positions' %d", groups_per_block, B, kv_heads);
     if (!projected || !keyed_templates || !q_gain || !k_gain || !out) return chess_fail(CHESS_INVALID_SHAPE, "template_attention: a required pointer is null");
     const int width = heads * dq + kv_heads * dq + kv_heads * dv + heads * templates_count;
     if (!aligned16(projected) || !aligned16(out) || !aligned16(keyed_templates) || width % 8 != 0)

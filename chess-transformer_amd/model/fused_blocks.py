@@ -24,7 +24,8 @@ LINEAR_DEPTH, GROUP_M = 32, 8
 FEATURE_SLOTS = 23
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
 LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 11)]}
-# positions a launch should reach before a workgroup takes several key/value groups
+# the workgroups an attention launch keeps while a workgroup takes as many (position, key/value group) pairs as it can:
+# a workgroup's start (its template registers and first loads) is paid once for its pairs
 ATTENTION_WORKGROUPS = 1024
 
 
@@ -40,12 +41,13 @@ def linear_tile(device: torch.device, M: int) -> int:
 
 
 def groups_per_workgroup(positions: int, kv_heads: int) -> int:
-    """The most key/value groups a workgroup takes while the launch keeps ATTENTION_WORKGROUPS workgroups; any choice gives the same bits."""
-    best = 1
-    for groups in range(1, kv_heads + 1):
-        if kv_heads % groups == 0 and positions * (kv_heads // groups) >= ATTENTION_WORKGROUPS:
-            best = groups
-    return best
+    """The most (position, key/value group) pairs a workgroup takes -- a divisor of all the launch's pairs -- while the launch keeps
+    ATTENTION_WORKGROUPS workgroups; any choice gives the same bits."""
+    pairs = positions * kv_heads
+    groups = max(1, pairs // ATTENTION_WORKGROUPS)
+    while pairs % groups:
+        groups -= 1
+    return groups
 
 
 def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, heads: int, kv_heads: int,

@@ -60,7 +60,8 @@ int chess_int8_matmul_i32(const void* x, const void* w, void* out, int M, int N,
 /* Template attention of B positions of T tokens (64 <= T <= 128): projected[B, T, H*dq | KV*dq | KV*dv | H*tc]
  * fp16, keyed_templates[64, 64, 8] fp16 (keyed[i][j][t] = templates[t][i][j] for t < tc, zero beyond; 16-byte
  * aligned), q_gain/k_gain[dq] fp16 -> out[B, T, H*dv] fp16; scale = 1/sqrt(dq).
- * groups_per_block key/value groups share a workgroup (any divisor of KV; it changes no bit).
+ * A workgroup takes groups_per_block (position, key/value group) pairs in a row, which may run across positions
+ * (any divisor of B * KV; it changes no bit).
  * Replaces template_attention_cuda (model/attention_cuda.py:97-304, launch :379-391, pointer order
  * projected, paired templates, q_gain, k_gain, out; templates paired once, :410-440) and the Triton pair
  * template_bias_kernel + template_attention_kernel (model/fused_blocks.py:35-171). */

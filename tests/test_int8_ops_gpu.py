@@ -381,9 +381,13 @@ def test_template_attention_reads_the_templates_and_their_coefficients(device):
 
 
 def test_groups_a_workgroup_change_no_bit(device):
+    """Any run of (position, key/value group) pairs a workgroup takes gives the same bits, runs across positions too (12: three
+    positions' 4 groups each; 36: all nine positions in one workgroup)."""
     arguments = attention_operands(device, 9, 8, 4, 32, 32, seed=3)
-    found = [launch_template_attention(*arguments, groups_per_block=groups) for groups in (1, 2, 4)]
+    found = [launch_template_attention(*arguments, groups_per_block=groups) for groups in (1, 2, 4, 3, 12, 36)]
     assert all(torch.equal(found[0], other) for other in found[1:])
+    with pytest.raises(ValueError):
+        launch_template_attention(*arguments, groups_per_block=5)   # not a divisor of the 36 pairs
 
 
 def test_template_attention_refuses_what_it_cannot_take(device):
