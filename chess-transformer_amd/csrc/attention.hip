@@ -10,15 +10,19 @@
 // model/attention_cuda.py:410-440).
 //
 // A workgroup takes a run of groups_per_block (position, key/value group) pairs, in order, which may run on
-// from one position into the next; it has one wavefront per slab of 16 queries. For each group the workgroup stages the normalised keys [key][dq] and the values,
-// transposed, [d][key] in LDS. A wavefront then runs each head of the group on v_mfma_f32_16x16x32_f16:
-// the scores come out transposed, S^T = K Q^T, so a lane holds one query's scores for 4 keys of each
-// 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B operand, so the probabilities
-// never leave registers. A lane keeps its query's templates for its 16 square keys in registers across
-// the heads, as f16 pairs: the bias of a key is 4 v_dot2_f32_f16 of them with the head's coefficients.
+// from one position into the next; it has one wavefront per slab of 16 queries. A group's raw key, value and
+// query rows arrive by DMA into LDS, double-buffered: the next group's rows load while this group's heads run.
+// A wavefront then runs each head of the group on v_mfma_f32_16x16x32_f16: the scores come out transposed,
+// S^T = K Q^T, from the raw keys and a per-key scale, so a lane holds one query's scores for 4 keys of each
+// 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B operand, so the probabilities never leave
+// registers. V^T's fragments are read from the raw value rows by transposing LDS reads (ds_read_b64_tr_b16: in
+// each 16 lanes, lane j receives element j % 4 of the 8 bytes lanes j / 4 + 4 r address, r = 0..3), so the
+// values are never transposed in LDS. The template bias is an MFMA too, from the templates held in registers.
 // Attention is held to a tolerance, not to bits: the norms take the hardware reciprocal square root, sums
 // of squares are v_dot2_f32_f16 of the fp16 pairs, and the softmax's exponent is one fma.
 #include "chess_common.h"
+
+#include <type_traits>
 
 namespace {
 
@@ -42,6 +46,26 @@ DEVICE uint4 lds_read16_settled(const LDS_SPACE void* p) {
     return uint4{v[0], v[1], v[2], v[3]};
 }
 
+// A transposing LDS read (ds_read_b64_tr_b16), issued as an instruction of its own: in each 16 lanes, lane j gets
+// element j % 4 of the 8 bytes that lanes j / 4, j / 4 + 4, j / 4 + 8 and j / 4 + 12 address, in that order. The
+// caller waits (lgkmcnt) before using the result: through the builtin, the compiler would first wait for every DMA
+// in flight (the next group's rows too), unable to tell the addresses apart.
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+template <int OFFSET> DEVICE v2u transposed_read(const LDS_SPACE int8_t* p) {
+    static_assert(OFFSET >= 0 && OFFSET < 65536, "an LDS instruction's offset");
+    v2u v;
+    asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"((uint32_t)(uintptr_t)p), "i"(OFFSET));
+    return v;
+}
+
+// f(std::integral_constant<int, I>()) for I = FIRST .. LAST - 1, in order: a loop whose index is a compile-time constant
+template <int FIRST, int LAST, typename F> DEVICE void each_step(F&& f) {
+    if constexpr (FIRST < LAST) {
+        f(std::integral_constant<int, FIRST>());
+        each_step<FIRST + 1, LAST>(f);
+    }
+}
+
 DEVICE void lds_write8(LDS_SPACE void* p, uint2 v) {
     asm volatile("ds_write_b64 %0, %1" : : "v"((uint32_t)(uintptr_t)p), "v"(v) : "memory");
 }
@@ -58,18 +82,15 @@ struct Layout {
     static constexpr int STEPS = (TILES + 1) / 2;     // 32-key steps of P V
     static constexpr int KEYS = TILES * 16;           // keys (and queries) staged
     static constexpr int VKEYS = STEPS * 32;          // value keys staged (P is zero past T)
-    static constexpr int V_ROW = VKEYS + 8;           // halves a transposed value column: 8 mod 16, so that the
-                                                      // transposing writes of key pairs spread over the banks
     static constexpr int KC = DQP / 8, VC = DV / 8;   // 16-byte chunks a raw key (query) row, a raw value row
-    // LDS in bytes: transposed values, two buffers of raw keys, raw values, the keys' scales, then two buffers of
-    // raw queries and template coefficients
-    static constexpr int VALUES_BYTES = DV * V_ROW * 2;
+    // LDS in bytes: two buffers of raw keys, two of raw values, the keys' scales, then two buffers of raw queries and
+    // template coefficients
     static constexpr int RAW_K_BYTES = KEYS * DQP * 2;   // a buffer's
-    static constexpr int RAW_V_BYTES = VKEYS * DV * 2;
+    static constexpr int RAW_V_BYTES = VKEYS * DV * 2;   // a buffer's
     static constexpr int SCALES_BYTES = KEYS * 4;
     static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
     static constexpr int COEF_BYTES = 64 * MAX_TEMPLATES * 2;   // a head's template coefficients, a square query a row
-    static constexpr int FIXED_BYTES = VALUES_BYTES + 2 * RAW_K_BYTES + RAW_V_BYTES + SCALES_BYTES;
+    static constexpr int FIXED_BYTES = 2 * RAW_K_BYTES + 2 * RAW_V_BYTES + SCALES_BYTES;
     static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * (RAW_Q_BYTES + COEF_BYTES); }
 };
 
@@ -115,9 +136,10 @@ struct DmaPlan {
 };
 
 // TILES = ceil(T / 16) exactly: the launch picks the instantiation, so every count below is fixed at compile time.
-// Registers are held to two wavefronts a SIMD, within which no instantiation needs scratch: a scratch reload would
-// wait for the DMA in flight too. (Fewer registers for more workgroups a CU cost more instructions than they gain:
-// the kernel is bound by its VALU work.)
+// Registers are held to two wavefronts a SIMD, within which the query and value widths up to 64 need no scratch (a
+// scratch reload would wait for the DMA in flight too); query widths of 128, and value widths of 128 past 96 tokens,
+// spill some. (Fewer registers for more workgroups a CU cost more instructions than they gain: the kernel is bound
+// by its VALU work.)
 template <int DQP, int DV, int TILES>
 __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2))) void template_attention_kernel(
     const half_t* __restrict__ projected, const half_t* __restrict__ keyed, const half_t* __restrict__ q_gain,
@@ -127,11 +149,10 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     typedef Layout<DQP, DV, TILES> L;
     constexpr int KC = L::KC, VC = L::VC, WAVES = TILES, THREADS = 64 * TILES, STEPS = L::STEPS, KEYS = L::KEYS;
     extern __shared__ __align__(16) int8_t lds[];
-    half_t* values = (half_t*)lds;
-    LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)(lds + L::VALUES_BYTES);   // [2][KEYS * DQP halves]
-    LDS_SPACE int8_t* raw_v = raw_k + 2 * L::RAW_K_BYTES;
-    float* key_scales = (float*)(lds + L::VALUES_BYTES + 2 * L::RAW_K_BYTES + L::RAW_V_BYTES);   // [KEYS]: the scale times the key's rsqrt
-    LDS_SPACE int8_t* raw_q = raw_v + L::RAW_V_BYTES + L::SCALES_BYTES;     // [2][per_kv][KEYS * DQP halves]
+    LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)lds;                        // [2][KEYS * DQP halves]
+    LDS_SPACE int8_t* raw_v = raw_k + 2 * L::RAW_K_BYTES;                    // [2][VKEYS * DV halves]
+    float* key_scales = (float*)(lds + 2 * L::RAW_K_BYTES + 2 * L::RAW_V_BYTES);   // [KEYS]: the scale times the key's rsqrt
+    LDS_SPACE int8_t* raw_q = raw_v + 2 * L::RAW_V_BYTES + L::SCALES_BYTES;  // [2][per_kv][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -155,13 +176,15 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     value_plan.plan(T - 1, width, slab, lane);
     const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
 
-    // a pair's keys, queries and coefficients (into a buffer), or its values
-    auto dma_group = [&](int pair, bool v, bool kq, int buffer) {
+    // a pair's keys and values (kv), its queries and coefficients (q), into a buffer
+    auto dma_group = [&](int pair, int buffer, bool kv, bool q) {
         const half_t* board = board_of(pair);
         const int group = pair % kv_heads;
-        if (v) value_plan.issue(raw_v, board + v_offset + group * DV, slab);
-        if (kq) {
+        if (kv) {
+            value_plan.issue(raw_v + buffer * L::RAW_V_BYTES, board + v_offset + group * DV, slab);
             key_plan.issue(raw_k + buffer * L::RAW_K_BYTES, board + k_offset + group * dq, slab);
+        }
+        if (q) {
             for (int hi = 0; hi < per_kv; hi++)
                 key_plan.issue(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, slab);
             if (templates_count == MAX_TEMPLATES) {
@@ -171,7 +194,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             }
         }
     };
-    dma_group(first_pair, true, true, 0);
+    dma_group(first_pair, 0, true, true);
 
     // The template bias of a 16-key tile is an MFMA too: bias^T[k][q] = sum over (q', t) of templates[t][q'][k] *
     // [q' == q] c[q][t], an inner dimension of the wavefront's 16 queries x 8 templates, 32 a step. In step j the A
@@ -205,8 +228,6 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     constexpr int PART_CHUNKS = KC / 4;
     static_assert(KEYS * 4 == THREADS && KC % 4 == 0, "four threads a key");
     const int scale_key = tid / 4, first_chunk = (tid % 4) * PART_CHUNKS;
-    // the value pairs this thread transposes: key pair item % (STEPS 16), chunk item / (STEPS 16)
-    constexpr int V_TOTAL = STEPS * 16 * VC, V_ITEMS = (V_TOTAL + THREADS - 1) / THREADS;
     // the staged outputs this thread writes out: row item / VC, chunk item % VC of each head
     constexpr int O_TOTAL = KEYS * VC, O_ITEMS = (O_TOTAL + THREADS - 1) / THREADS;
     const float inverse_dq = 1.0f / (float)dq;
@@ -243,9 +264,11 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
         // this group's raw rows have landed (this wavefront's DMA), and every wavefront is past the previous group
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        // the previous group's outputs leave its query buffer before the next group's queries come into it
+        // the next group's keys and values load into the other buffers (every wavefront is past their last reads);
+        // the previous group's outputs leave its query buffer, which takes the next group's queries once every
+        // wavefront has read its share (after the barrier below)
+        if (gi + 1 < groups_per_block) dma_group(pair + 1, buffer ^ 1, true, false);
         if (STAGED && gi > 0) write_out(pair - 1, buffer ^ 1);
-        if (gi + 1 < groups_per_block) dma_group(pair + 1, false, true, buffer ^ 1);
 
         // the keys' scales: scale * rsqrt(mean of squares + eps) over the key's dq columns. Past dq a raw key chunk
         // holds another head's columns: zeroed here, as a zero query column would not cancel an infinite one.
@@ -266,26 +289,8 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             squares += lane_xor2(squares);
             if (tid % 4 == 0) key_scales[scale_key] = __builtin_amdgcn_rsqf(squares * inverse_dq + eps) * scale;
         }
-        // values, transposed to [d][key] a key pair at a time (4-byte writes)
-#pragma unroll
-        for (int k = 0; k < V_ITEMS; k++) {
-            const int item = tid + k * THREADS;
-            if (V_TOTAL % THREADS != 0 && item >= V_TOTAL) break;
-            const int kp = item % (STEPS * 16), c = item / (STEPS * 16), key = 2 * kp;
-            const v4u lo = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key, c) * 16);
-            const v4u hi = *reinterpret_cast<const LDS_SPACE v4u*>(raw_v + raw_slot<VC>(key + 1, c) * 16);
-            const uint32_t lo_words[4] = {lo[0], lo[1], lo[2], lo[3]}, hi_words[4] = {hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-            for (int e = 0; e < 8; e++) {
-                // element e of a row is half e % 2 of its word e / 2
-                const uint32_t first = e % 2 ? lo_words[e / 2] >> 16 : lo_words[e / 2] & 0xFFFFu;
-                const uint32_t second = e % 2 ? hi_words[e / 2] >> 16 : hi_words[e / 2] & 0xFFFFu;
-                *reinterpret_cast<uint32_t*>(values + (c * 8 + e) * L::V_ROW + key) = first | (second << 16);
-            }
-        }
-        lds_barrier();
-        // the raw values are read: the next group's come in while this one's heads run
-        if (gi + 1 < groups_per_block) dma_group(pair + 1, true, false, 0);
+        lds_barrier();   // the keys' scales (and zeroed chunks) are in place, and every wavefront's outputs are read
+        if (gi + 1 < groups_per_block) dma_group(pair + 1, buffer ^ 1, false, true);
 
         for (int hi = 0; hi < per_kv; hi++) {
             const int head = group * per_kv + hi;
@@ -389,12 +394,22 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             total += __shfl_xor(total, 32, 64);
             const float inverse_total = __builtin_amdgcn_rcpf(total);
 
-            // O^T = V^T P^T over 32-key steps: position e of both operands is key 32 st + 16 (e / 4) + 4 quad + e % 4
+            // O^T = V^T P^T over 32-key steps: position e of both operands is key 32 st + 16 (e / 4) + 4 quad + e % 4.
+            // V^T's half h (positions 4 h ..) of lane (col, quad) is V[32 st + 16 h + 4 quad + r][16 dt + col], r = 0..3:
+            // a transposing read in which lane 4 r' + g of the 16 addresses the 4 values of key 32 st + 16 h + 4 quad + r',
+            // columns 16 dt + 4 g .. + 3 (half g % 2 of chunk 2 dt + g / 2).
+            // the swizzle of a row repeats every 16 rows, so the rows 16 h + 32 st on are the lane's first at a fixed offset
+            const LDS_SPACE int8_t* values = raw_v + buffer * L::RAW_V_BYTES;
+            const int value_row = 4 * quad + col / 4, value_group = col % 4;
+            const LDS_SPACE int8_t* value_base[DV / 16];
+#pragma unroll
+            for (int dt = 0; dt < DV / 16; dt++)
+                value_base[dt] = values + raw_slot<VC>(value_row, 2 * dt + value_group / 2) * 16 + (value_group % 2) * 8;
             v4f o[DV / 16];
 #pragma unroll
             for (int dt = 0; dt < DV / 16; dt++) o[dt] = v4f{0, 0, 0, 0};
-#pragma unroll
-            for (int st = 0; st < STEPS; st++) {
+            each_step<0, STEPS>([&](auto st_index) {
+                constexpr int st = decltype(st_index)::value, ROW_BYTES = VC * 16;
                 __builtin_amdgcn_sched_barrier(0);
                 v8h pf;
 #pragma unroll
@@ -402,15 +417,22 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                     pf[r] = (half_t)s[2 * st][r];
                     pf[4 + r] = (half_t)s[2 * st + 1][r];
                 }
+                // the step's reads go out together, then one wait for them all
+                v2u halves[DV / 16][2];
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
-                    const half_t* row = values + (dt * 16 + col) * L::V_ROW + st * 32 + quad * 4;
-                    const v4h lo = *reinterpret_cast<const v4h*>(row);
-                    const v4h hi = *reinterpret_cast<const v4h*>(row + 16);
+                    halves[dt][0] = transposed_read<32 * st * ROW_BYTES>(value_base[dt]);
+                    halves[dt][1] = transposed_read<(32 * st + 16) * ROW_BYTES>(value_base[dt]);
+                }
+                asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+                for (int dt = 0; dt < DV / 16; dt++) {
+                    asm volatile("" : "+v"(halves[dt][0]), "+v"(halves[dt][1]));
+                    const v4h lo = __builtin_bit_cast(v4h, halves[dt][0]), hi = __builtin_bit_cast(v4h, halves[dt][1]);
                     const v8h vf = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
                     o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
                 }
-            }
+            });
             if constexpr (STAGED) {
                 // over this query's own row of the head's queries: columns 16 dt + 4 quad .. + 4 are chunk 2 dt + quad / 2
                 LDS_SPACE int8_t* row = raw_q + (buffer * per_kv + hi) * head_bytes;

@@ -141,9 +141,9 @@ template <int C, bool QUANT>
 int launch(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
            void* q, void* scale, void* normed, int M, int D, float eps, hipStream_t stream)
 {
-    // rows a wavefront: enough loads in flight to stream at HBM speed once the launch fills the chip, one row a
-    // wavefront while it does not
-    constexpr int WIDE = C <= 8 ? 4 : 2;
+    // rows a wavefront: two once the launch fills the chip (at 71,680 rows of 512 one row takes 41.5 us, two 29.1, four
+    // 30.0, eight 31.2 on an MI355X), one row a wavefront while it does not
+    constexpr int WIDE = 2;
     const bool wide = M >= 32768;
     const int rows_per_block = WAVES * (wide ? WIDE : 1);
     const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);

@@ -24,6 +24,9 @@ LINEAR_DEPTH, GROUP_M = 32, 8
 FEATURE_SLOTS = 23
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers
 LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 11)]}
+# f32 out (accumulate_fp32, the policy head's `a`): its f32 staging runs faster at 128 x 128 with a 3-stage ring (78 against
+# 97 us at 71,680 rows on an MI355X)
+LINEAR_F32_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
 # the workgroups an attention launch keeps while a workgroup takes as many (position, key/value group) pairs as it can:
 # a workgroup's start (its template registers and first loads) is paid once for its pairs
 ATTENTION_WORKGROUPS = 1024
@@ -35,9 +38,10 @@ def tile_for(tiles: list[tuple[float, object]], M: int, multiprocessors: int):
     return next(tile for most, tile in tiles if share <= most)
 
 
-def linear_tile(device: torch.device, M: int) -> int:
+def linear_tile(device: torch.device, M: int, accumulate_fp32: bool = False) -> int:
     arch = torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
-    return tile_for(LINEAR_TILES.get(arch, LINEAR_TILES["gfx950"]), M, torch.cuda.get_device_properties(device).multi_processor_count)
+    table = LINEAR_F32_TILES if accumulate_fp32 else LINEAR_TILES
+    return tile_for(table.get(arch, table["gfx950"]), M, torch.cuda.get_device_properties(device).multi_processor_count)
 
 
 def groups_per_workgroup(positions: int, kv_heads: int) -> int:
@@ -168,7 +172,7 @@ def launch_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
            gated: bool = False, accumulate_fp32: bool = False, original: torch.Tensor | None = None, residual_scale: torch.Tensor | None = None,
            input_scale: torch.Tensor | None = None) -> torch.Tensor:
-    tile = linear_tile(x.device, x.numel() // weight.shape[0])
+    tile = linear_tile(x.device, x.numel() // weight.shape[0], accumulate_fp32)
     return launch_linear(x, weight, bias, residual, gated, accumulate_fp32, original, residual_scale, input_scale, tile)
 
 

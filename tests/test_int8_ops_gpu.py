@@ -305,6 +305,22 @@ def test_int8_linear_writes_bf16(device):
     assert np.array_equal(cpu(out.float()), expected)
 
 
+ALL_TILES = tuple(range(1, 12))   # 12 is the gated-only streamed kernel, tested on its own
+
+
+@pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])
+def test_every_tile_gives_the_same_bits(device, matmul):
+    """Every tile of the int8 GEMM and of its fp16 instance, partial last tiles in rows (210) and columns (200): one set of bits."""
+    operands = int8_operands(matmul, 210, device)
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
+    outputs = [launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile) for tile in ALL_TILES]
+    assert all(same_bits(out, outputs[0]) for out in outputs[1:])
+    halves = x.half()
+    w16 = (weight.float().t() / 128).half().contiguous()
+    fp16 = [launch_linear(halves, w16, bias, residual, gated, False, *mix, tile) for tile in ALL_TILES]
+    assert all(same_bits(out, fp16[0]) for out in fp16[1:])
+
+
 def test_the_op_picks_a_tile_and_keeps_the_bits(device):
     operands = int8_operands("down", 140, device)
     x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
@@ -355,6 +371,19 @@ def test_template_attention_is_the_attention_in_fp32(device, heads, kv_heads, dq
     expected = reference_attention(arguments)
     assert out.dtype == torch.float16 and out.shape == expected.shape
     assert torch.allclose(out.float(), expected, atol=1e-2)
+    rounded = oracle.template_attention(*(cpu(t) if isinstance(t, torch.Tensor) else t for t in arguments))
+    assert np.abs(cpu(out.float()) - rounded).max() < 4e-3
+
+
+@pytest.mark.parametrize("heads, kv_heads, dq, dv", [(8, 8, 64, 128), (8, 4, 32, 16), (4, 4, 64, 64)])
+@pytest.mark.parametrize("tokens", [70, 100, 128])
+def test_template_attention_at_every_value_width_and_token_count(device, heads, kv_heads, dq, dv, tokens):
+    """The value rows read transposed for the P V products: value widths 16 to 128 (2 to 16 chunks a row), 5 to 8 tiles of 16
+    tokens, against the reference's fp32 formula."""
+    arguments = attention_operands(device, 3, heads, kv_heads, dq, dv, seed=tokens + dv, tokens=tokens)
+    out = template_attention(*arguments)
+    expected = reference_attention(arguments)
+    assert out.shape == expected.shape and torch.allclose(out.float(), expected, atol=1e-2)
     rounded = oracle.template_attention(*(cpu(t) if isinstance(t, torch.Tensor) else t for t in arguments))
     assert np.abs(cpu(out.float()) - rounded).max() < 4e-3
 
