@@ -110,25 +110,32 @@ template <> DEVICE void stage_four<bf16_t>(bf16_t* to, const float (&v)[4]) {
 }
 template <typename OutT> DEVICE void stage_four(OutT*, const float (&)[4]) {}
 
+// A stage is SK bytes of K: 64 (16 rows a 1 KB block, 4 lanes a row) or 128 (8 rows a block, 8 lanes a row, so that a
+// DMA instruction reads whole 128-byte lines: the L2 serves 128-byte lines, and with 64-byte stages each line of an
+// operand row is read twice, a step apart). A lane's 16-byte chunk of a row sits at chunk ^ swizzle(row) of its row's
+// slots: over the 16 rows an MFMA operand group reads, the chunks fall in 16 different 16-byte bank groups.
+template <int SK> constexpr int block_rows() { return BLOCK / SK; }
+template <int SK> DEVICE int chunk_swizzle(int row) { return SK == 64 ? (row & 15) >> 2 : (row & 15) >> 1; }
+
 // An f32 staged tile (an epilogue that still adds to it) is staged half its rows at a time when every wavefront
 // has two or more row fragments: half the LDS, so that more workgroups fit a CU.
 template <int BM, int WAVES_M, bool PACKED> constexpr int staging_halves() { return !PACKED && (BM / WAVES_M / 32) % 2 == 0 ? 2 : 1; }
 
 // LDS: the ring of stages, reused after the main loop for the staged output tile; then the epilogue's column
 // and row vectors (f32: NB x BN weight scales and BM row scales for int8, BN bias)
-template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED, int SK = 64>
 constexpr int vector_offset() {
-    constexpr int RING = STAGES * (BM / 16 + NB * BN / 16) * BLOCK;
+    constexpr int RING = STAGES * (BM / block_rows<SK>() + NB * BN / block_rows<SK>()) * BLOCK;
     constexpr int STAGING = PACKED ? BM * (BN + 8) * 2 : BM / staging_halves<BM, WAVES_M, PACKED>() * (BN + 4) * 4;
     return RING > STAGING ? RING : STAGING;
 }
-template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED>
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED, int SK = 64>
 constexpr int lds_bytes() {
     constexpr bool SCALED = std::is_same<In, int8_t>::value && !std::is_same<OutT, int>::value;
-    return vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
+    return vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI, int SK = 64>
 __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
 {
@@ -137,9 +144,11 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     constexpr bool INT8 = std::is_same<In, int8_t>::value;
     constexpr bool RAW = std::is_same<OutT, int>::value;
     constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
-    constexpr int A_BLOCKS = BM / 16, B_BLOCKS = NB * BN / 16, BLOCKS = A_BLOCKS + B_BLOCKS;
+    constexpr int ROWS_A_BLOCK = block_rows<SK>(), CHUNKS = SK / 16, SUBS = SK / 32;
+    constexpr int A_BLOCKS = BM / ROWS_A_BLOCK, B_BLOCKS = NB * BN / ROWS_A_BLOCK, BLOCKS = A_BLOCKS + B_BLOCKS;
     constexpr int PER_WAVE = BLOCKS / 4;
     constexpr int STAGE_BYTES = BLOCKS * BLOCK;
+    static_assert(SK == 64 || SK == 128, "stages of 64 or 128 bytes");
     static_assert(BLOCKS % 4 == 0 && FM >= 1 && FN >= 1, "tile shape");
     extern __shared__ __align__(16) int8_t lds[];
 
@@ -150,7 +159,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     // the epilogue's flags: fixed by the instantiation (EPI >= 0, the network's combinations), else read at run time
     const int flags = EPI >= 0 ? EPI : e.flags;
     const size_t row_bytes = (size_t)K * sizeof(In);
-    const int steps = (int)(row_bytes / STAGE_K_BYTES);
+    const int steps = (int)(row_bytes / SK);
 
     const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
     const int tile = xcd_local_tile(blockIdx.x, tiles_m * tiles_n);
@@ -161,16 +170,17 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     const int m0 = (first_m + tile % in_group % group_rows) * BM;
     const int n0 = (tile % in_group / group_rows) * BN;
 
-    // this lane's source in each of the wavefront's blocks: row lane / 4 of the block, 16-byte chunk (lane % 4) ^ (lane / 16).
-    // Rows past M read row M - 1 and columns past N read column N - 1: their sums are never stored.
+    // this lane's source in each of the wavefront's blocks: row lane / CHUNKS of the block, 16-byte chunk
+    // (lane % CHUNKS) ^ swizzle(row). Rows past M read row M - 1 and columns past N read column N - 1: their sums are
+    // never stored.
     // A block's source is a scalar base (x or w, the block index being the same in all lanes) plus a 32-bit lane
     // offset, so that the step's loads take the scalar-base form with no per-step address arithmetic in the lanes.
     uint32_t source[PER_WAVE];
 #pragma unroll
     for (int p = 0; p < PER_WAVE; p++) {
         const int block = wave * PER_WAVE + p;
-        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * 16 + (lane >> 2);
-        const int chunk = ((lane & 3) ^ ((lane >> 4) & 3)) * 16;
+        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * ROWS_A_BLOCK + lane / CHUNKS;
+        const int chunk = ((lane % CHUNKS) ^ chunk_swizzle<SK>(row)) * 16;
         if (block < A_BLOCKS) {
             source[p] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)row_bytes + chunk;
         } else {
@@ -250,7 +260,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     // the DMA of step into ring stage S (S == step % STAGES, fixed at compile time)
     auto issue = [&](int step, auto stage_index) {
         constexpr int S = decltype(stage_index)::value;
-        const int k0 = min(step, steps - 1) * STAGE_K_BYTES;
+        const int k0 = min(step, steps - 1) * SK;
 #pragma unroll
         for (int p = 0; p < PER_WAVE; p++)
             buffer_dma16(wave * PER_WAVE + p < A_BLOCKS ? x_rsrc : w_rsrc, (LDS_SPACE void*)(ring + S * STAGE_BYTES + (wave * PER_WAVE + p) * BLOCK),
@@ -260,16 +270,17 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     typename MMA::Acc acc[NB][FM][FN];
 
     // an operand lane (row lane % 32, 16-byte half lane / 32 of each 32-byte sub-step) in a stage: the block of its
-    // 16 rows, then the slot 4 r + (chunk ^ (r / 4)) of row r's chunk
-    const int in_row = lane & 31, half = lane >> 5, r16 = in_row & 15;
+    // row, then the slot CHUNKS r + (chunk ^ swizzle(r)) of row r's chunk
+    const int in_row = lane & 31, half = lane >> 5;
     // a lane's operand addresses in stage 0: this wavefront's A rows and B columns (the fragment and stage offsets
     // are then immediates)
-    int a_operand[2], b_operand[2];
+    int a_operand[SUBS], b_operand[SUBS];
 #pragma unroll
-    for (int sub = 0; sub < 2; sub++) {
-        const int operand = (in_row >> 4) * BLOCK + (r16 * 4 + ((half + 2 * sub) ^ (r16 >> 2))) * 16;
-        a_operand[sub] = operand + (wm * WM / 16) * BLOCK;
-        b_operand[sub] = operand + (A_BLOCKS + wn * WN / 16) * BLOCK;
+    for (int sub = 0; sub < SUBS; sub++) {
+        const int operand = (in_row / ROWS_A_BLOCK) * BLOCK
+                          + ((in_row % ROWS_A_BLOCK) * CHUNKS + ((half + 2 * sub) ^ chunk_swizzle<SK>(in_row))) * 16;
+        a_operand[sub] = operand + (wm * WM / ROWS_A_BLOCK) * BLOCK;
+        b_operand[sub] = operand + (A_BLOCKS + wn * WN / ROWS_A_BLOCK) * BLOCK;
     }
 
     static_for<0, STAGES - 1>([&](auto s) { issue(decltype(s)::value, s); });
@@ -278,17 +289,17 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         constexpr bool FIRST = decltype(first_step)::value;
         constexpr int STAGE = decltype(stage_index)::value * STAGE_BYTES;
 #pragma unroll
-        for (int sub = 0; sub < 2; sub++) {
+        for (int sub = 0; sub < SUBS; sub++) {
             typename MMA::Operand af[FM];
 #pragma unroll
             for (int i = 0; i < FM; i++)
-                af[i] = *(const LDS_SPACE typename MMA::Operand*)(ring + a_operand[sub] + STAGE + (i * 32 / 16) * BLOCK);
+                af[i] = *(const LDS_SPACE typename MMA::Operand*)(ring + a_operand[sub] + STAGE + (i * 32 / ROWS_A_BLOCK) * BLOCK);
 #pragma unroll
             for (int g = 0; g < NB; g++)
 #pragma unroll
                 for (int j = 0; j < FN; j++) {
                     const typename MMA::Operand bf =
-                        *(const LDS_SPACE typename MMA::Operand*)(ring + b_operand[sub] + STAGE + ((g * BN + j * 32) / 16) * BLOCK);
+                        *(const LDS_SPACE typename MMA::Operand*)(ring + b_operand[sub] + STAGE + ((g * BN + j * 32) / ROWS_A_BLOCK) * BLOCK);
 #pragma unroll
                     for (int i = 0; i < FM; i++)
                         acc[g][i][j] = MMA::step(bf, af[i], FIRST && sub == 0 ? typename MMA::Acc{} : acc[g][i][j]);
@@ -317,7 +328,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
     asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
     if constexpr (NORM) asm volatile("" : "+v"(gain_bits));
-    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>());
+    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>());
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++)
         if (const int at = tid + v * THREADS; at < VEC) {
@@ -482,10 +493,12 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     }
 }
 
-template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI>
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI, int SK = 64>
 int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
-    constexpr int BYTES = lds_bytes<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED>();
-    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED, EPI>;
+    if (((size_t)K * sizeof(In)) % SK != 0)
+        return chess_fail(CHESS_UNSUPPORTED, "a tile of %d-byte stages reads rows of a multiple of %d bytes, not %d", SK, SK, (int)(K * sizeof(In)));
+    constexpr int BYTES = lds_bytes<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>();
+    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED, EPI, SK>;
     if (BYTES > 65536) {
         static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
         if (allowed != hipSuccess) return (int)allowed;
@@ -495,7 +508,7 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
     return launch_status();
 }
 
-constexpr int TILES = 12;
+constexpr int TILES = 13;
 
 // The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
@@ -503,6 +516,7 @@ constexpr int TILES = 12;
 // 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
 // 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2). 0 picks by the launch's size.
 // 12 is the persistent gated GEMM of gemm_stream.hip (256 x 64, a 4-stage ring running across tiles), gated fp16 only.
+// 13: 128 x 128 (2 x 2, 2) with stages of 128 bytes of K (rows of a multiple of 128 bytes).
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
@@ -516,6 +530,7 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
         case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 9: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 10: return launch<In, 256, 64, 4, 1, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 13: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);
         default: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
     }
 }

@@ -26,10 +26,11 @@ INT8_DEPTH = 64
 # The GEMM's tiles by the rows a compute unit's share is (the reference's table format, int8_blocks.py:19-31), timed on an
 # MI355X: 1 is 64 x 64, 2 128 x 128, 3 128 x 64, 4 256 x 128, 5 128 x 256, 6 256 x 64 (rows x outputs, a 4-stage ring),
 # 7 128 x 128, 8 128 x 64, 9 256 x 64 (a 3-stage ring), 10 256 x 64, 11 128 x 128 (a 2-stage ring: three workgroups a
-# compute unit, which is what the batch-1024 network runs fastest with). Every tile gives the same bits.
+# compute unit, which is what the batch-1024 network runs fastest with), 13 128 x 128 (a 2-stage ring of 128-byte stages:
+# down's 2,048-byte rows, read in whole L2 lines). Every tile gives the same bits.
 INT8_TILES = {"gfx950": {"projection": [(4, 1), (math.inf, 11)],
                          "gate_up": [(4, 1), (math.inf, 10)],
-                         "down": [(32, 1), (math.inf, 11)]}}
+                         "down": [(32, 1), (math.inf, 13)]}}
 # rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit
 NORM_ROWS = 4
 ROTATE_ROWS = 4

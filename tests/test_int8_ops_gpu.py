@@ -305,7 +305,7 @@ def test_int8_linear_writes_bf16(device):
     assert np.array_equal(cpu(out.float()), expected)
 
 
-ALL_TILES = tuple(range(1, 12))   # 12 is the gated-only streamed kernel, tested on its own
+ALL_TILES = (*range(1, 12), 13)   # 12 is the gated-only streamed kernel, tested on its own; 13 takes 128-byte stages
 
 
 @pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])
@@ -319,6 +319,14 @@ def test_every_tile_gives_the_same_bits(device, matmul):
     w16 = (weight.float().t() / 128).half().contiguous()
     fp16 = [launch_linear(halves, w16, bias, residual, gated, False, *mix, tile) for tile in ALL_TILES]
     assert all(same_bits(out, fp16[0]) for out in fp16[1:])
+
+
+def test_128_byte_stages_refuse_rows_of_64(device):
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("projection", 70, device, width=128, depth=192)
+    launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 1)   # 64-byte stages take it
+    for tile in (13,):
+        with pytest.raises(ValueError):
+            launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
 
 
 def test_the_op_picks_a_tile_and_keeps_the_bits(device):
