@@ -27,6 +27,10 @@ LINEAR_TILES = {"gfx950": [(4, 1), (math.inf, 11)]}
 # f32 out (accumulate_fp32, the policy head's `a`): its f32 staging runs faster at 128 x 128 with a 3-stage ring (78 against
 # 97 us at 71,680 rows on an MI355X)
 LINEAR_F32_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
+# rows of 2 KB or more (the fp16 block's down, 2,048 inputs), not gated: 128 x 128 with 128-byte stages, whole L2 lines a
+# step (190 against 226 us at 71,680 rows)
+LINEAR_LONG_ROW_TILES = {"gfx950": [(4, 1), (math.inf, 13)]}
+LONG_ROW_BYTES = 2048
 # the workgroups an attention launch keeps while a workgroup takes as many (position, key/value group) pairs as it can:
 # a workgroup's start (its template registers and first loads) is paid once for its pairs
 ATTENTION_WORKGROUPS = 1024
@@ -38,9 +42,14 @@ def tile_for(tiles: list[tuple[float, object]], M: int, multiprocessors: int):
     return next(tile for most, tile in tiles if share <= most)
 
 
-def linear_tile(device: torch.device, M: int, accumulate_fp32: bool = False) -> int:
+def linear_tile(device: torch.device, M: int, accumulate_fp32: bool = False, row_bytes: int = 0, gated: bool = False) -> int:
     arch = torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
-    table = LINEAR_F32_TILES if accumulate_fp32 else LINEAR_TILES
+    if accumulate_fp32:
+        table = LINEAR_F32_TILES
+    elif row_bytes >= LONG_ROW_BYTES and row_bytes % 128 == 0 and not gated:
+        table = LINEAR_LONG_ROW_TILES
+    else:
+        table = LINEAR_TILES
     return tile_for(table.get(arch, table["gfx950"]), M, torch.cuda.get_device_properties(device).multi_processor_count)
 
 
@@ -174,7 +183,7 @@ def launch_linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | No
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, residual: torch.Tensor | None = None,
            gated: bool = False, accumulate_fp32: bool = False, original: torch.Tensor | None = None, residual_scale: torch.Tensor | None = None,
            input_scale: torch.Tensor | None = None) -> torch.Tensor:
-    tile = linear_tile(x.device, x.numel() // weight.shape[0], accumulate_fp32)
+    tile = linear_tile(x.device, x.numel() // weight.shape[0], accumulate_fp32, weight.shape[0] * x.element_size(), gated)
     return launch_linear(x, weight, bias, residual, gated, accumulate_fp32, original, residual_scale, input_scale, tile)
 
 
