@@ -45,8 +45,10 @@ int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int wi
 /* out[M, N] = epilogue(x[M, K] @ w[N(x2 if gated), K]^T) with x, w int8 and exact int32 sums;
  * epilogue: dequantise by x_scale[M] and w_scale[N(x2)], + bias[N], silu(gate) * up when gated,
  * + residual[M, N], then the next block's input mix when original != NULL; fp16 or bf16 out.
- * K % 64 == 0. tile: 0 picks by size; 1..9 force 64x64, 128x128, 128x64, 256x128, 128x256, 256x64 (rows x
- * outputs), then 128x128, 128x64, 256x64 with a shallower ring; no tile changes a bit.
+ * K % 64 == 0. tile: 0 picks by size; 1..11 force 64x64, 128x128, 128x64, 256x128, 128x256, 256x64 (rows x
+ * outputs), then 128x128, 128x64, 256x64 with a 3-stage ring and 256x64, 128x128 with a 2-stage ring; 12 the
+ * persistent gated GEMM (gated, fp16 out, nothing added); 13 128x128 with 128-byte stages (K a multiple of 128
+ * bytes). No tile changes a bit.
  * Pointer order of small_int8 (model/int8_cuda.py:35-39); replaces int8_linear_kernel
  * and small_int8 (model/int8_blocks.py:66-144, model/int8_cuda.py:34-183, :362-383). */
 int chess_int8_linear(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* bias, const void* residual,
