@@ -16,7 +16,7 @@ CSRC = Path(__file__).resolve().parent
 PACKAGE = CSRC.parent
 LIBRARY = PACKAGE / "libchess_hip.so"
 OBJECTS = CSRC / "_build"
-SOURCES = ["runtime.hip", "norm_quant.hip", "rotate_quant.hip", "gemm.hip", "gemm_stream.hip", "attention.hip", "embedding.hip", "heads.hip"]
+SOURCES = ["runtime.hip", "norm_quant.hip", "rotate_quant.hip", "gemm.hip", "gemm_stream.hip", "attention.hip", "embedding.hip", "heads.hip", "answers.hip"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off and IEEE divide/sqrt: the f32 op order the kernels declare is what runs.

@@ -28,6 +28,14 @@ CASTLING_TOKEN_OFFSET = TURN_TOKEN_OFFSET + NUM_FLAG_VALUES
 EN_PASSANT_TOKEN_OFFSET = CASTLING_TOKEN_OFFSET + NUM_FLAG_VALUES
 BOARD_VOCAB_SIZE = EN_PASSANT_TOKEN_OFFSET + NUM_SQUARES
 
+# the start position's tokens, white to move (piece codes 1-6 pawn..king of the side to move, 7-12 the other side's),
+# every castling right, no en-passant square: what encode_board(chess.Board()) gives (reference encoding.py:6-23); the
+# engine's graph lanes record on it (reference engine/inference.py:92-93)
+START_POSITION_TOKENS = (
+    (4, 2, 3, 5, 6, 3, 2, 4) + (1,) * 8 + (0,) * 32 + (7,) * 8 + (10, 8, 9, 11, 12, 9, 8, 10)
+    + (TURN_TOKEN_OFFSET + 1,) + (CASTLING_TOKEN_OFFSET + 1,) * 4 + (EN_PASSANT_TOKEN_OFFSET,)
+)
+
 # python-chess piece numbers, which the promotion table is ordered and offset by
 KNIGHT_PIECE, BISHOP_PIECE, ROOK_PIECE, QUEEN_PIECE = 2, 3, 4, 5
 QUEEN_LINES = [(0, 1), (0, -1), (1, 0), (-1, 0), (1, 1), (-1, 1), (1, -1), (-1, -1)]

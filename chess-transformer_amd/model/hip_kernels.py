@@ -33,6 +33,7 @@ SIGNATURES = {
     "chess_int8_linear_norm_quant": [_pointer] * 12 + [_int] * 3 + [_float, _pointer],
     "chess_board_embedding": [_pointer, _int] + [_pointer] * 7 + [_int] * 12 + [_pointer],
     "chess_move_logits": [_pointer] * 9 + [_int] * 6 + [_pointer],
+    "chess_lean_answers": [_pointer] * 4 + [_int] * 5 + [_pointer],
     "chess_runtime_addresses": [ctypes.POINTER(ctypes.c_void_p), _int],
     "chess_error_string": [_int],
     "chess_last_error": [],

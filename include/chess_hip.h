@@ -114,6 +114,14 @@ int chess_board_embedding(const void* boards, int code_bytes, const void* rays, 
 int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
                       const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves, void* stream);
 
+/* The lean lanes' answers (engine/inference.py:131-137, Lane.answer's gather on a lean lane): rows[B][row_bytes] hold
+ * at byte columns_at `columns` little-endian int16 indices into a board's answer row, the moves' logits then the
+ * expected score (:19-23; the row layout of engine/selfplay_rs/src/lib.rs:331-333). answers[B][columns] f32 =
+ * index < moves ? logits[b][index] (logits f32 [B][moves]) : score[b] (f32 [B]); an index outside [0, moves] gives
+ * NaN. Replaces the torch.cat of the answer rows and the torch.gather. rows, row_bytes and columns_at even. */
+int chess_lean_answers(const void* logits, const void* score, const void* rows, void* answers, int B, int moves, int row_bytes,
+                       int columns_at, int columns, void* stream);
+
 /* Fills table[0..6] with hipSetDevice, hipMemcpyAsync, hipGraphLaunch, hipEventRecord, hipEventSynchronize,
  * hipStreamSynchronize, hipGetErrorString: the address table of engine/cuda_runtime.py:17-49 (CudaRuntime.CALLS
  * and addresses()), whose HIP functions have the CUDA ones' signatures; the native round loop

@@ -89,12 +89,19 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 4, 512, 100, 1e-5, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, 16, None, None, 16, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, None, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
+    # the lean answers: the indices inside the row, even rows and places, every pointer
+    assert library.chess_lean_answers(16, 16, 16, 16, 4, 1968, 508, 70, 220, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_lean_answers(16, 16, 16, 16, 4, 0, 508, 70, 219, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_lean_answers(16, 16, None, 16, 4, 1968, 508, 70, 219, None) == hip_kernels.INVALID_SHAPE
+    assert library.chess_lean_answers(16, 16, 16, 16, 4, 1968, 509, 70, 219, None) == hip_kernels.MISALIGNED
+    assert library.chess_lean_answers(16, 16, 17, 16, 4, 1968, 508, 70, 219, None) == hip_kernels.MISALIGNED
 
 
 def test_empty_batches_launch_nothing(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_rms_norm(16, None, None, None, 16, None, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, 0, 70, 512, 21, 5, 1968, None) == 0
+    assert library.chess_lean_answers(16, 16, 16, 16, 0, 1968, 508, 70, 219, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
     assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 0, 512, 64, 1e-5, None) == 0
     assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 0, 512, 128, 1e-5, None) == 0

@@ -1,0 +1,202 @@
+"""The engine's graph lanes and their lean answer rows (the reference's engine/inference.py:25-235 and its
+tests/test_inference.py:57-278): graph sizes and chunks on the CPU; on the GPU, the lean gather kernel against the
+reference's torch.cat + torch.gather, and lanes of graphs of the int8 network against the network run eagerly."""
+import math
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from engine import inference
+from engine.inference import (ANSWER_WIDTH, LEAN_COLUMNS, LEAN_ROW, GraphedBatches, ImmediateBatches, answer_rows, graph_sizes,
+                              int8_network, lean_answers, small_graph_sizes)
+from engine.quantization import nearest_int8_weights
+from model.encoding import NUM_MOVE_IDS, START_POSITION_TOKENS, TOKENS_PER_BOARD
+
+
+@pytest.mark.parametrize("max_batch, chunk", [(64, None), (300, None), (64, 64), (256, 64), (300, 48)])
+def test_small_graph_sizes_pad_little(max_batch, chunk):
+    sizes = small_graph_sizes(max_batch, chunk)
+    assert sizes == sorted(set(sizes)) and sizes[0] == 1 and sizes[-1] >= max_batch
+    every = chunk or max_batch
+    for batch in range(1, max_batch + 1):
+        padded = next(size for size in sizes if size >= batch)
+        # no batch pads into a chunk of its own, and past 16 boards a chunk's last part pads by less than a sixteenth
+        assert math.ceil(padded / every) == math.ceil(batch / every)
+        last = padded - (padded - 1) // every * every
+        if last > 16:
+            assert padded - batch < max(4, last // 16)
+    assert all(whole in sizes for whole in range(every, max_batch + 1, every))
+
+
+def test_graph_sizes_step_by_64_then_128_then_256():
+    sizes = graph_sizes(2600)
+    assert sizes[0] == 64 and sizes[-1] >= 2600 > sizes[-2]
+    steps = {size: later - size for size, later in zip(sizes, sizes[1:])}
+    assert all(step == (64 if size < 1024 else 128 if size < 2048 else 256) for size, step in steps.items())
+
+
+# the reference's expected chunks (tests/test_inference.py:71-76)
+@pytest.mark.parametrize("l2_mb, width, lanes, chunk", [(96, 768, 2, 64), (96, 768, 1, 128), (48, 768, 2, 64), (48, 256, 2, 96),
+                                                        (48, 128, 2, 192), (6, 768, 1, 64)])
+def test_chunk_positions_fit_the_l2(monkeypatch, l2_mb, width, lanes, chunk):
+    monkeypatch.setattr(torch.cuda, "current_device", lambda: 0)
+    monkeypatch.setattr(torch.cuda, "get_device_properties", lambda device: SimpleNamespace(L2_cache_size=l2_mb << 20))
+    assert inference.chunk_positions(width, lanes) == chunk
+
+
+def test_the_lean_row_is_the_native_crates():
+    # engine/selfplay_rs/src/lib.rs:330-333 of the reference: 218 legal-move slots, the expected score last; 70 token bytes
+    assert (LEAN_COLUMNS, LEAN_ROW, ANSWER_WIDTH) == (219, 508, 1969) and ANSWER_WIDTH == NUM_MOVE_IDS + 1
+
+
+def test_the_start_position_tokens():
+    # the reference's START_POSITION_ENCODING (tests/test_board_encoding.py:43-52), its token numbers written out
+    expected = [4, 2, 3, 5, 6, 3, 2, 4] + [1] * 8 + [0] * 32 + [7] * 8 + [10, 8, 9, 11, 12, 9, 8, 10] + [14] + [16] * 4 + [17]
+    assert list(START_POSITION_TOKENS) == expected and len(expected) == TOKENS_PER_BOARD
+
+
+def test_immediate_batches_answer_at_launch():
+    batches = ImmediateBatches(lambda boards: boards.sum(axis=1, keepdims=True))
+    boards = np.arange(6).reshape(2, 3)
+    assert np.array_equal(batches.collect(batches.launch(boards)), [[3], [12]])
+
+
+# --- on the GPU ---
+
+def whole_rows(logits: torch.Tensor, score: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """The reference's lean answers (engine/inference.py:134-137), on the CPU: the answer rows, then a gather at the indices."""
+    columns = rows[:, TOKENS_PER_BOARD:].contiguous().view(torch.int16).long()
+    return torch.cat([logits, score.unsqueeze(1)], dim=1).gather(1, columns)
+
+
+def lean_input(boards: torch.Tensor, columns: torch.Tensor) -> torch.Tensor:
+    rows = torch.zeros(len(boards), LEAN_ROW, dtype=torch.uint8)
+    rows[:, :TOKENS_PER_BOARD] = boards
+    rows[:, TOKENS_PER_BOARD:] = columns.to(torch.int16).view(torch.uint8).reshape(len(boards), -1)
+    return rows
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("B", [1, 37, 1024])
+def test_lean_answers_are_the_gather_of_the_answer_rows(device, B):
+    generator = torch.Generator().manual_seed(B)
+    logits, score = torch.randn(B, NUM_MOVE_IDS, generator=generator), torch.randn(B, generator=generator)
+    columns = torch.randint(0, ANSWER_WIDTH, (B, LEAN_COLUMNS), generator=generator)
+    columns[:, -1] = ANSWER_WIDTH - 1
+    rows = lean_input(torch.randint(0, 81, (B, TOKENS_PER_BOARD), generator=generator), columns)
+    answers = lean_answers(logits.to(device), score.to(device), rows.to(device), TOKENS_PER_BOARD, LEAN_COLUMNS).cpu()
+    assert torch.equal(answers, whole_rows(logits, score, rows))
+
+
+@pytest.mark.gpu
+def test_lean_answers_of_indices_past_the_row_are_nan(device):
+    logits, score = torch.randn(2, NUM_MOVE_IDS), torch.randn(2)
+    columns = torch.full((2, LEAN_COLUMNS), 5)
+    columns[0, 3], columns[1, 7] = -1, ANSWER_WIDTH
+    rows = lean_input(torch.zeros(2, TOKENS_PER_BOARD, dtype=torch.long), columns)
+    answers = lean_answers(logits.to(device), score.to(device), rows.to(device), TOKENS_PER_BOARD, LEAN_COLUMNS).cpu()
+    assert answers[0, 3].isnan() and answers[1, 7].isnan()
+    assert answers[0, 4] == logits[0, 5] and answers[1, 6] == logits[1, 5]
+
+
+@pytest.mark.gpu
+def test_lean_answers_refuse_odd_rows(device):
+    rows = torch.zeros(2, LEAN_ROW + 1, dtype=torch.uint8, device=device)
+    with pytest.raises(ValueError, match="even"):
+        lean_answers(torch.zeros(2, 10, device=device), torch.zeros(2, device=device), rows, TOKENS_PER_BOARD, LEAN_COLUMNS)
+
+
+def random_boards(count: int, seed: int) -> np.ndarray:
+    generator = torch.Generator().manual_seed(seed)
+    boards = torch.randint(0, 13, (count, TOKENS_PER_BOARD), generator=generator)
+    boards[:, 64:] = torch.tensor(START_POSITION_TOKENS[64:])
+    return boards.numpy()
+
+
+@pytest.fixture(scope="module")
+def network():
+    from test_network_gpu import SMALL, make_model
+    device = torch.device("cuda", torch.cuda.current_device())
+    return int8_network(make_model(SMALL).to(device), nearest_int8_weights(make_model(SMALL)))
+
+
+def eager_rows(network, boards: np.ndarray) -> np.ndarray:
+    with torch.no_grad():
+        return answer_rows(network(torch.from_numpy(boards).cuda())).cpu().numpy()
+
+
+@pytest.mark.gpu
+def test_graphs_answer_like_the_network(network):
+    boards = random_boards(5, 1)
+    graphs = GraphedBatches(network, [2, 8])
+    answers = graphs.collect(graphs.launch(boards)).copy()
+    expected = eager_rows(network, boards)
+    # the move logits bit for bit; the expected score through the eval head's BLAS calls, whose kernels may differ by batch
+    assert np.array_equal(answers[:, :-1], expected[:, :-1])
+    assert np.allclose(answers[:, -1], expected[:, -1], rtol=0, atol=1e-6)
+
+
+@pytest.mark.gpu
+def test_more_batches_out_than_lanes_are_refused(network):
+    boards = random_boards(1, 2)
+    graphs = GraphedBatches(network, [1], in_flight=1)
+    launched = graphs.launch(boards)
+    with pytest.raises(RuntimeError, match="more batches in flight than lanes"):
+        graphs.launch(boards)
+    graphs.collect(launched)
+    graphs.collect(graphs.launch(boards))
+
+
+@pytest.mark.gpu
+def test_batches_are_collected_in_any_order(network):
+    boards = random_boards(3, 3)
+    graphs = GraphedBatches(network, [1, 2])
+    expected = graphs.collect(graphs.launch(boards[1:])).copy()
+    first, second = graphs.launch(boards[:1]), graphs.launch(boards[1:])
+    graphs.collect(second)
+    third = graphs.launch(boards[1:])
+    graphs.collect(first)
+    assert np.array_equal(graphs.collect(third), expected)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("blocking_wait", [False, True])
+def test_lean_lanes_answer_the_columns_of_whole_rows(network, blocking_wait):
+    whole = GraphedBatches(network, [8, 16], 2, blocking_wait=blocking_wait)
+    lean = GraphedBatches(network, [8, 16], 2, blocking_wait=blocking_wait, lean=True)
+    random = np.random.default_rng(4)
+    for count in (12, 5, 16):
+        boards = random_boards(count, count)
+        columns = random.integers(0, ANSWER_WIDTH, size=(count, LEAN_COLUMNS))
+        columns[:, -1] = ANSWER_WIDTH - 1
+        lane = lean.free_lane()
+        lane.rows_array[:count] = lean_input(torch.from_numpy(boards), torch.from_numpy(columns)).numpy()
+        rows = whole.collect(whole.launch(boards)).copy()
+        answers = lean.collect(lean.launch_filled(lane, count)).copy()
+        assert np.array_equal(answers, np.take_along_axis(rows, columns, axis=1))
+
+
+@pytest.mark.gpu
+def test_batches_in_flight_together_answer_as_alone(network):
+    batches = random_boards(512, 5).reshape(2, 256, -1)
+    alone = GraphedBatches(network, [256], in_flight=1)
+    expected = [alone.collect(alone.launch(batch)).copy() for batch in batches]
+    together = GraphedBatches(network, [256])
+    for _ in range(5):
+        launched = [together.launch(batch) for batch in batches]
+        assert np.array_equal([together.collect(one).copy() for one in launched], expected)
+
+    columns = np.random.default_rng(6).integers(0, ANSWER_WIDTH, size=(2, 256, LEAN_COLUMNS))
+    rows = np.stack([lean_input(torch.from_numpy(batch), torch.from_numpy(batch_columns)).numpy()
+                     for batch, batch_columns in zip(batches, columns)])
+    expected = [np.take_along_axis(rows_alone, batch_columns, axis=1) for rows_alone, batch_columns in zip(expected, columns)]
+    lean = GraphedBatches(network, [256], lean=True)
+    for _ in range(5):
+        launched = []
+        for batch_rows in rows:
+            lane = lean.free_lane()
+            lane.rows_array[:256] = batch_rows
+            launched.append(lean.launch_filled(lane, 256))
+        assert np.array_equal([lean.collect(one).copy() for one in launched], expected)
