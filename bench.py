@@ -389,10 +389,12 @@ def main() -> int:
     if arguments.sweep:
         for batch in (1, 16, 64, 256, 1024, 4096):
             graphed = Graphed(network, batch, device)
-            ms, replays = time_graph(graphed, 20, 3)
+            ms, replays = time_graph(graphed, 200, 10)
             replays.sort()
-            sweep[batch] = {"ms_per_batch": round(ms, 4), "p50_ms": round(replays[len(replays) // 2], 4), "positions_per_s": round(batch / ms * 1e3, 1)}
-            log(f"  sweep batch {batch}: {ms:.3f} ms, {batch / ms * 1e3:,.0f} positions/s")
+            p50, p99 = replays[len(replays) // 2], replays[int(len(replays) * 0.99) - 1]
+            sweep[batch] = {"ms_per_batch": round(ms, 4), "p50_ms": round(p50, 4), "p99_ms": round(p99, 4),
+                            "positions_per_s": round(batch / ms * 1e3, 1)}
+            log(f"  sweep batch {batch}: {ms:.3f} ms, p50 {p50:.3f} ms, p99 {p99:.3f} ms, {batch / ms * 1e3:,.0f} positions/s")
             del graphed
 
     roofline = dominant_kernel(device, network, arguments.batch)
