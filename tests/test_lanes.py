@@ -200,3 +200,29 @@ def test_batches_in_flight_together_answer_as_alone(network):
             lane.rows_array[:256] = batch_rows
             launched.append(lean.launch_filled(lane, 256))
         assert np.array_equal([lean.collect(one).copy() for one in launched], expected)
+
+
+def test_serve_answers_each_slot_its_boards():
+    """serve on the CPU with ImmediateBatches: each search's request (a count of boards in its slot) is answered in its
+    slot's array, and the counters add up (reference engine/inference.py:36-59)."""
+    import threading
+    from multiprocessing import Pipe
+
+    from engine.inference import serve
+
+    pairs = [Pipe() for _ in range(3)]
+    boards = [np.full((4, TOKENS_PER_BOARD), slot, dtype=np.uint8) for slot in range(3)]
+    answers = [np.zeros((4, 1), dtype=np.float32) for _ in range(3)]
+    stop, calls, positions = threading.Event(), SimpleNamespace(value=0), SimpleNamespace(value=0)
+    network = ImmediateBatches(lambda batch: batch[:, :1].astype(np.float32) * 10)
+    server = threading.Thread(target=serve, args=(network, boards, answers, [served for served, _ in pairs], stop, calls, positions))
+    server.start()
+    try:
+        for slot, count in ((0, 2), (2, 4), (1, 1)):
+            pairs[slot][1].send(count)
+            assert pairs[slot][1].poll(10) and pairs[slot][1].recv() is True
+            assert np.array_equal(answers[slot][:count], np.full((count, 1), 10 * slot))
+    finally:
+        stop.set()
+        server.join(10)
+    assert positions.value == 7 and calls.value >= 1
