@@ -46,12 +46,13 @@ template <int C, bool VECTOR> DEVICE void load_raw(const half_t* row, int col, i
     }
 }
 
-template <int C> DEVICE void widen(const half_t (&raw)[C], int col, int D, float (&out)[C]) {
+// FULL: the row is exactly 64 lanes of C (D == 64 C), so no element is past the row and nothing is masked
+template <int C, bool FULL> DEVICE void widen(const half_t (&raw)[C], int col, int D, float (&out)[C]) {
 #pragma unroll
-    for (int i = 0; i < C; i++) out[i] = col + i < D ? (float)raw[i] : 0.0f;
+    for (int i = 0; i < C; i++) out[i] = FULL || col + i < D ? (float)raw[i] : 0.0f;
 }
 
-template <int C, int R, bool VECTOR, bool QUANT>
+template <int C, int R, bool VECTOR, bool QUANT, bool FULL = false>
 __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
     const half_t* __restrict__ x, const half_t* __restrict__ original, const half_t* __restrict__ residual_scale,
     const half_t* __restrict__ input_scale, const half_t* __restrict__ gain, half_t* __restrict__ mixed,
@@ -71,10 +72,12 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
         load_raw<C, VECTOR>(x + (size_t)row * D, col, D, raw_x[r]);
         if (mix) load_raw<C, VECTOR>(original + (size_t)row * D, col, D, raw_o[r]);
     }
+    // the gain: one vector load when the row is full (the launch checks its alignment), else element by element
     half_t raw_g[C];
-    load_raw<C, false>(gain, col, D, raw_g);
+    if constexpr (FULL) copy_bytes<2 * C>(raw_g, gain + col);
+    else load_raw<C, false>(gain, col, D, raw_g);
     float g[C];
-    widen<C>(raw_g, col, D, g);
+    widen<C, FULL>(raw_g, col, D, g);
     float rs = 0.0f, is = 0.0f;
     if (mix) {
         rs = (float)residual_scale[0];
@@ -87,10 +90,10 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
         if (row >= M) break;
         const size_t base = (size_t)row * D;
         float v[C];
-        widen<C>(raw_x[r], col, D, v);
+        widen<C, FULL>(raw_x[r], col, D, v);
         if (mix) {
             float o[C];
-            widen<C>(raw_o[r], col, D, o);
+            widen<C, FULL>(raw_o[r], col, D, o);
             half_t m[C];
 #pragma unroll
             for (int i = 0; i < C; i++) {
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
                 v[i] = (float)m[i];
             }
             if (vector) {
-                if (col < D) copy_bytes<2 * C>(mixed + base + col, m);
+                if (FULL || col < D) copy_bytes<2 * C>(mixed + base + col, m);
             } else {
 #pragma unroll
                 for (int i = 0; i < C; i++)
@@ -110,7 +113,7 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
             int8_t out[C];
             const float absmax = norm_quant_row<C>(v, g, D, eps, out);
             if (vector) {
-                if (col < D) copy_bytes<C>(q + base + col, out);
+                if (FULL || col < D) copy_bytes<C>(q + base + col, out);
             } else {
 #pragma unroll
                 for (int i = 0; i < C; i++)
@@ -127,7 +130,7 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
                 out[i] = (half_t)y;
             }
             if (vector) {
-                if (col < D) copy_bytes<2 * C>(normed + base + col, out);
+                if (FULL || col < D) copy_bytes<2 * C>(normed + base + col, out);
             } else {
 #pragma unroll
                 for (int i = 0; i < C; i++)
@@ -147,8 +150,13 @@ int launch(const void* x, const void* original, const void* residual_scale, cons
     const bool wide = M >= 32768;
     const int rows_per_block = WAVES * (wide ? WIDE : 1);
     const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);
-    auto kernel = wide ? (D % C == 0 ? norm_quant_kernel<C, WIDE, true, QUANT> : norm_quant_kernel<C, WIDE, false, QUANT>)
-                       : (D % C == 0 ? norm_quant_kernel<C, 1, true, QUANT> : norm_quant_kernel<C, 1, false, QUANT>);
+    // a full row (D == 64 C) with a 16-byte aligned gain takes no masks and loads the gain as vectors (at 71,680 rows
+    // of 512 on an MI355X: 28.8 us, from 32.5 us with the masks and the gain's element loads)
+    const bool full = D == 64 * C && aligned16(gain);
+    auto kernel = wide ? (full ? norm_quant_kernel<C, WIDE, true, QUANT, true>
+                               : D % C == 0 ? norm_quant_kernel<C, WIDE, true, QUANT> : norm_quant_kernel<C, WIDE, false, QUANT>)
+                       : (full ? norm_quant_kernel<C, 1, true, QUANT, true>
+                               : D % C == 0 ? norm_quant_kernel<C, 1, true, QUANT> : norm_quant_kernel<C, 1, false, QUANT>);
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, (const half_t*)x, (const half_t*)original, (const half_t*)residual_scale,
                        (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q, (float*)scale, (half_t*)normed, M, D,
                        eps, original != nullptr ? 1 : 0);
