@@ -1,9 +1,12 @@
 // Fused template attention over one position's T tokens (64 squares, then T - 64 metadata tokens).
 // Computes what model/fused_blocks.py:35-97 (template_bias_kernel + template_attention_kernel) and
-// model/attention_cuda.py:97-304 compute, for any head counts and widths:
-//   q = f16(RMSNorm_head(q) * q_gain), k = f16(RMSNorm_head(k) * k_gain)    (f32 norms)
-//   s[i, j] = (q_i . k_j) * scale + [i, j < 64] f16(sum_t c[b, i, h, t] templates[t, i, j])
+// model/attention_cuda.py:97-304 compute, for any head counts and widths, in this order (which differs from the
+// reference's only in where fp16 roundings fall, and is held to its tolerance):
+//   q' = f16((q * rsqrt(mean(q^2) + eps)) * (q_gain * k_gain))     the key gain moved to the query side
+//   r_j = rsqrt(mean(k_j^2) + eps)                                  one scale a raw key; keys are never normalised
+//   s[i, j] = (q'_i . k_j) * r_j * scale + [i, j < 64] f16(sum_t c[b, i, h, t] templates[t, i, j])
 //   out_i = sum_j f16(exp(s_ij - max_i)) v_j / sum_j exp(s_ij - max_i)
+// (the reference rounds the normalised keys to fp16 and multiplies by the gains on the key side).
 // projected[B, T, H*dq | KV*dq | KV*dv | H*tc] in, out[B, T, H*dv] (fp16). The templates come key-major,
 // keyed[i][j][t] (8 templates a key, zero past templates_count), so that a lane reads its query's
 // templates for 4 keys as 4 16-byte loads (the reference pairs its templates likewise,

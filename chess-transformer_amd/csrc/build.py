@@ -16,22 +16,20 @@ CSRC = Path(__file__).resolve().parent
 PACKAGE = CSRC.parent
 LIBRARY = PACKAGE / "libchess_hip.so"
 OBJECTS = CSRC / "_build"
-SOURCES = ["runtime.hip", "norm_quant.hip", "rotate_quant.hip", "gemm.hip", "gemm_stream.hip", "attention.hip", "embedding.hip", "heads.hip", "answers.hip"]
+SOURCES = ["runtime.hip", "norm_quant.hip", "rotate_quant.hip", "gemm.hip", "attention.hip", "embedding.hip", "heads.hip", "answers.hip"]
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off and IEEE divide/sqrt: the f32 op order the kernels declare is what runs.
 # -packed-fp32-ops off: hipcc would otherwise pair f32 ops into v_pk_* instructions by itself.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-ffp-contract=off", "-fhip-fp32-correctly-rounded-divide-sqrt",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops", "-Wall", "-Wno-unused-function"]
-# MFMA results in ordinary VGPRs: no accumulator-register copies before the epilogue reads them. Not for the streamed
-# GEMM, whose two tiles' sums fill the accumulation registers.
+# MFMA results in ordinary VGPRs: no accumulator-register copies before the epilogue reads them.
 VGPR_FORM = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
-OWN_REGISTERS = {"gemm_stream.hip"}
 
 
 def compile_one(source: str) -> Path:
     target = OBJECTS / (Path(source).stem + ".o")
-    command = [HIPCC, *FLAGS, *([] if source in OWN_REGISTERS else VGPR_FORM), "-c", str(CSRC / source), "-o", str(target)]
+    command = [HIPCC, *FLAGS, *VGPR_FORM, "-c", str(CSRC / source), "-o", str(target)]
     result = subprocess.run(command, capture_output=True, text=True)
     if result.returncode != 0:
         raise RuntimeError(f"hipcc failed on {source}:\n{result.stdout}{result.stderr}")

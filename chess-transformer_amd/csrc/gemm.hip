@@ -37,17 +37,13 @@
 
 #include <type_traits>
 
-// gemm_stream.hip: the persistent gated GEMM (tile 12)
-int launch_gated_stream(const void* x, const void* w, void* out, const float* x_scale, const float* w_scale, int M, int N, int K,
-                        hipStream_t stream);
-
 namespace {
 
 constexpr int STAGE_K_BYTES = 64;
 constexpr int THREADS = 256;
 constexpr int BLOCK = 1024;      // bytes a DMA instruction writes: 16 rows x 64 bytes
 
-enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4, EPI_NORM = 8 };
+enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4 };
 
 struct Epilogue {
     const float* x_scale;        // int8 only
@@ -58,11 +54,6 @@ struct Epilogue {
     const half_t* residual_scale;
     const half_t* input_scale;
     int flags;
-    // EPI_NORM (whole-row tiles only): the fp16 output rows also leave as norm_quant's q[M, N] and scale[M]
-    const half_t* norm_gain;
-    int8_t* norm_q;
-    float* norm_scale;
-    float norm_eps;
 };
 
 typedef int v16i __attribute__((ext_vector_type(16)));
@@ -217,11 +208,6 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
     }
     constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = BM / ROWS;
-    // EPI_NORM: a wavefront's phase-2 pass holds one whole output row, 8 columns a lane, the layout norm_quant takes
-    constexpr bool NORM = EPI >= 0 && (EPI & EPI_NORM);
-    static_assert(!NORM || (ROW_LANES == 64 && !RAW && !PACKED && std::is_same<OutT, half_t>::value), "a normalised row is one wavefront's");
-    v4u gain_bits = {0u, 0u, 0u, 0u};   // the lane's 8 gains, raw
-    if constexpr (NORM) gain_bits = *reinterpret_cast<const v4u*>(e.norm_gain + lane * 8);
     // Staged in halves, half h holds row fragments h * HALF_FM .. of every wavefront: staged row r is tile row
     // (r / HALF_ROWS) * WM + h * HALF_ROWS + r % HALF_ROWS.
     constexpr int HALVES = staging_halves<BM, WAVES_M, PACKED>(), HALF_FM = FM / HALVES, HALF_ROWS = WM / HALVES;
@@ -233,13 +219,10 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     };
     constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
     // The residual / original rows of phase 2, held in registers: all of them loaded now while they fit beside the sums
-    // (8 passes, 64 registers at most); in the whole-row tile (16 passes, staged in halves), the first half's rows now and
-    // the second half's once the first half is staged (its sums then dead). A pass's own loads would wait: they cannot
-    // move above the previous pass's stores, which the compiler cannot tell apart from them. (The other tiles of more
-    // than 8 passes read in phase 2: with held rows the compiler fails on the gated 256 x 128 tile.)
-    constexpr bool PREFETCH = ADDS && PASSES <= 8;
-    constexpr bool AHEAD = NORM && HALVES == 2 && HALF_PASSES <= 8;
-    constexpr bool HELD = PREFETCH || AHEAD;
+    // (8 passes, 64 registers at most). A pass's own loads would wait: they cannot move above the previous pass's stores,
+    // which the compiler cannot tell apart from them. (Tiles of more than 8 passes read in phase 2: with held rows the
+    // compiler fails on the gated 256 x 128 tile.)
+    constexpr bool HELD = ADDS && PASSES <= 8;
     const bool vectors = N % 8 == 0;
     v8h residual_rows[HELD ? PASSES : 1], original_rows[HELD ? PASSES : 1];
     auto load_rows = [&](int pass) {
@@ -249,7 +232,7 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
     };
     if constexpr (HELD) {
 #pragma unroll
-        for (int pass = 0; pass < (PREFETCH ? PASSES : HALF_PASSES); pass++) load_rows(pass);
+        for (int pass = 0; pass < PASSES; pass++) load_rows(pass);
     }
 
     LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
@@ -327,7 +310,6 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
     asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
-    if constexpr (NORM) asm volatile("" : "+v"(gain_bits));
     float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>());
 #pragma unroll
     for (int v = 0; v < VEC_PER_THREAD; v++)
@@ -399,12 +381,6 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
         }
         __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
         bare_barrier();
-        if constexpr (AHEAD) {
-            if (h == 0) {
-#pragma unroll
-                for (int pass = HALF_PASSES; pass < PASSES; pass++) load_rows(pass);
-            }
-        }
 
         // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
         // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
@@ -465,22 +441,6 @@ __global__ __launch_bounds__(THREADS) void gemm_kernel(
 #pragma unroll
                     for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
                 }
-                if constexpr (NORM) {
-                    // norm_quant of the row as stored: the fp16-rounded values (the row is the wavefront's, m the same in every lane)
-                    const v8h gain = __builtin_bit_cast(v8h, gain_bits);
-                    float stored[8], g[8];
-                    int8_t q8[8];
-#pragma unroll
-                    for (int c = 0; c < 8; c++) {
-                        stored[c] = (float)(half_t)value[c];
-                        g[c] = (float)gain[c];
-                    }
-                    const float absmax = norm_quant_row<8>(stored, g, N, e.norm_eps, q8);
-                    store_eight<OutT>(out + at, value);
-                    *reinterpret_cast<v2u*>(e.norm_q + at) = __builtin_bit_cast(v2u, q8);
-                    if (lane == 0) e.norm_scale[m] = absmax / 127.0f;
-                    continue;
-                }
                 if (vectors) {
                     store_eight<OutT>(out + at, value);
                 } else {
@@ -514,9 +474,8 @@ constexpr int TILES = 13;
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
 // 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
-// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2). 0 picks by the launch's size.
-// 12 is the persistent gated GEMM of gemm_stream.hip (256 x 64, a 4-stage ring running across tiles), gated fp16 only.
-// 13: 128 x 128 (2 x 2, 2) with stages of 128 bytes of K (rows of a multiple of 128 bytes).
+// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2)  13: 128 x 128 (2 x 2, 2) with stages of 128 bytes of K (rows of a
+// multiple of 128 bytes). 0 picks by the launch's size; 12 is not a tile.
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
@@ -535,48 +494,35 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
     }
 }
 
-// A 16-bit output with nothing left to add is staged already rounded (half the LDS of the f32 staging).
+// The tile for tile 0: large launches take the 2-stage 128 x 128, with 128-byte stages for rows of 2 KB or more that
+// are a multiple of 128 bytes (each L2 line of an operand row read once); smaller ones the 4-stage tiles that still
+// give the chip a workgroup a compute unit.
+template <typename In> int tile_by_size(int M, int N, int K) {
+    const size_t row_bytes = (size_t)K * sizeof(In);
+    if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 512) return row_bytes >= 2048 && row_bytes % 128 == 0 ? 13 : 11;
+    if ((long)((M + 127) / 128) * ((N + 127) / 128) >= 256) return 2;
+    return (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
+}
+
+// The epilogues the network and the standalone configs use are built with their flags fixed, for fp16 and bf16 outputs
+// alike; any other combination reads them at run time. A 16-bit output with nothing left to add is staged already
+// rounded (half the LDS of the f32 staging).
 template <typename In, int NB, typename OutT>
 int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
-    if (tile == 0) {
-        const long large = (long)((M + 255) / 256) * ((N + 127) / 128);
-        tile = large >= 512 ? 11 : (long)((M + 127) / 128) * ((N + 127) / 128) >= 256 ? 2 : (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
-    }
-    // the network's epilogues are built with their flags fixed; any other combination reads them at run time
+    if (tile == 0) tile = tile_by_size<In>(M, N, K);
+    if (tile == 12) return chess_fail(CHESS_UNSUPPORTED, "tile 12 is not a tile of this GEMM");
     const int f = e.flags;
-    if (tile == 12) {
-        if constexpr (std::is_same<In, int8_t>::value && NB == 2 && std::is_same<OutT, half_t>::value) {
-            if (f == 0) return launch_gated_stream(x, w, out, e.x_scale, e.w_scale, M, N, K, stream);
-        }
-        return chess_fail(CHESS_UNSUPPORTED, "tile 12 is the streamed gated GEMM: int8 in, fp16 out, gated, no bias or residual");
-    }
-    if constexpr (std::is_same<OutT, half_t>::value) {
-        if (NB == 2 && f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);
-        if (NB == 1 && f == EPI_BIAS) return by_tile<In, NB, OutT, true, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);
-        if (NB == 1 && f == EPI_RESIDUAL) return by_tile<In, NB, OutT, false, EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
-        if (NB == 1 && f == (EPI_RESIDUAL | EPI_MIX)) return by_tile<In, NB, OutT, false, EPI_RESIDUAL | EPI_MIX>(x, w, out, e, M, N, K, tile, stream);
-        if (NB == 1 && f == (EPI_BIAS | EPI_RESIDUAL)) return by_tile<In, NB, OutT, false, EPI_BIAS | EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
-    }
     if constexpr (sizeof(OutT) == 2) {
+        if (f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);
+        if constexpr (NB == 1) {
+            if (f == EPI_BIAS) return by_tile<In, NB, OutT, true, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);
+            if (f == EPI_RESIDUAL) return by_tile<In, NB, OutT, false, EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+            if (f == (EPI_RESIDUAL | EPI_MIX)) return by_tile<In, NB, OutT, false, EPI_RESIDUAL | EPI_MIX>(x, w, out, e, M, N, K, tile, stream);
+            if (f == (EPI_BIAS | EPI_RESIDUAL)) return by_tile<In, NB, OutT, false, EPI_BIAS | EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+        }
         if (!(f & (EPI_RESIDUAL | EPI_MIX))) return by_tile<In, NB, OutT, true, -1>(x, w, out, e, M, N, K, tile, stream);
     }
     return by_tile<In, NB, OutT, false, -1>(x, w, out, e, M, N, K, tile, stream);
-}
-
-// EPI_NORM's whole-row tile: 64 rows x 512 outputs, 1 x 4 wavefronts, 2 stages (76 KB of LDS, so two workgroups a
-// CU); phase 2 gives each wavefront one whole row a pass.
-constexpr int NORM_WIDTH = 512;
-template <typename In, int EPI>
-int launch_normalised(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
-    static_assert(EPI & EPI_NORM, "the whole-row tile is for the normalising epilogue");
-    return launch<In, 64, NORM_WIDTH, 1, 4, 1, 2, half_t, false, EPI>(x, w, out, e, M, N, K, stream);
-}
-
-int check_norm(const void* residual, const void* gain, const void* q, const void* scale, int N, const char* what) {
-    if (!residual || !gain || !q || !scale) return chess_fail(CHESS_INVALID_SHAPE, "%s needs the residual, the gain, q and scale", what);
-    if (N != NORM_WIDTH) return chess_fail(CHESS_UNSUPPORTED, "%s normalises rows of %d outputs, not %d", what, NORM_WIDTH, N);
-    if (!aligned16(gain) || !aligned16(q)) return chess_fail(CHESS_MISALIGNED, "%s reads the gain and writes q 16 and 8 bytes a lane", what);
-    return CHESS_OK;
 }
 
 int check(const void* x, const void* w, void* out, int M, int N, int K, int depth, int tile, const char* what) {
@@ -647,35 +593,4 @@ extern "C" int chess_linear(const void* x, const void* w, const void* bias, cons
                                     : dispatch<half_t, 2, float>(x, w, out, e, M, N, K, tile, s);
     }
     return out_dtype == OUT_F16 ? dispatch<half_t, 1, half_t>(x, w, out, e, M, N, K, tile, s) : dispatch<half_t, 1, float>(x, w, out, e, M, N, K, tile, s);
-}
-
-extern "C" int chess_linear_norm_quant(const void* x, const void* w, const void* bias, const void* residual, const void* gain, void* out,
-                                       void* q, void* scale, int M, int N, int K, float eps, void* stream)
-{
-    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES / 2, 0, "linear_norm_quant")) return status;
-    if (int status = check_epilogue(bias, residual, nullptr, nullptr, nullptr, "linear_norm_quant")) return status;
-    if (int status = check_norm(residual, gain, q, scale, N, "linear_norm_quant")) return status;
-    if (M == 0) return CHESS_OK;
-    Epilogue e{nullptr, nullptr, (const half_t*)bias, (const half_t*)residual, nullptr, nullptr, nullptr, 0,
-               (const half_t*)gain, (int8_t*)q, (float*)scale, eps};
-    hipStream_t s = (hipStream_t)stream;
-    if (bias) return launch_normalised<half_t, EPI_BIAS | EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
-    return launch_normalised<half_t, EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
-}
-
-extern "C" int chess_int8_linear_norm_quant(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* residual,
-                                            const void* original, const void* residual_scale, const void* input_scale, const void* gain,
-                                            void* out, void* q, void* scale, int M, int N, int K, float eps, void* stream)
-{
-    if (int status = check(x, w, out, M, N, K, STAGE_K_BYTES, 0, "int8_linear_norm_quant")) return status;
-    if (int status = check_epilogue(nullptr, residual, original, residual_scale, input_scale, "int8_linear_norm_quant")) return status;
-    if (int status = check_norm(residual, gain, q, scale, N, "int8_linear_norm_quant")) return status;
-    if (!x_scale || !w_scale) return chess_fail(CHESS_INVALID_SHAPE, "int8_linear_norm_quant needs both scales");
-    if (!aligned16(w_scale)) return chess_fail(CHESS_MISALIGNED, "int8_linear_norm_quant reads the weight scales 4 at a time");
-    if (M == 0) return CHESS_OK;
-    Epilogue e{(const float*)x_scale, (const float*)w_scale, nullptr, (const half_t*)residual, (const half_t*)original,
-               (const half_t*)residual_scale, (const half_t*)input_scale, 0, (const half_t*)gain, (int8_t*)q, (float*)scale, eps};
-    hipStream_t s = (hipStream_t)stream;
-    if (original) return launch_normalised<int8_t, EPI_RESIDUAL | EPI_MIX | EPI_NORM>(x, w, out, e, M, N, K, s);
-    return launch_normalised<int8_t, EPI_RESIDUAL | EPI_NORM>(x, w, out, e, M, N, K, s);
 }

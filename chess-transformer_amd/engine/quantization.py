@@ -25,7 +25,7 @@ from torch import nn
 
 from model.checkpoint import load_model
 from model.fused_blocks import link_input_mixes
-from model.int8_blocks import DOWN_INPUT_MULTIPLE, HADAMARD_BLOCK, Int8Block, down_inputs, hadamard, link_norm_handoffs
+from model.int8_blocks import DOWN_INPUT_MULTIPLE, HADAMARD_BLOCK, Int8Block, down_inputs, hadamard
 from model.model import ChessTransformer
 
 Int8Weights = dict[int, dict[str, tuple[torch.Tensor, torch.Tensor]]]
@@ -190,7 +190,6 @@ def block_errors(checkpoint_path: Path, weights: Int8Weights, boards: torch.Tens
     def priors(int8_blocks: dict[int, nn.Module]) -> torch.Tensor:
         blocks = [int8_blocks.get(layer, block) for layer, block in enumerate(fp16_blocks)]
         link_input_mixes(blocks)
-        link_norm_handoffs(blocks)
         model.encoder = nn.ModuleList(blocks)
         logits = torch.cat([answer_rows(model(boards[start:start + ERROR_BATCH]))[:, :-1] for start in range(0, len(boards), ERROR_BATCH)])
         return torch.softmax(logits.double().masked_fill(~legal, -torch.inf), dim=-1)

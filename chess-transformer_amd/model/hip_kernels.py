@@ -29,8 +29,6 @@ SIGNATURES = {
     "chess_int8_matmul_i32": [_pointer] * 3 + [_int] * 4 + [_pointer],
     "chess_template_attention": [_pointer] * 5 + [_int] * 8 + [_float, _float, _pointer],
     "chess_linear": [_pointer] * 8 + [_int] * 6 + [_pointer],
-    "chess_linear_norm_quant": [_pointer] * 8 + [_int] * 3 + [_float, _pointer],
-    "chess_int8_linear_norm_quant": [_pointer] * 12 + [_int] * 3 + [_float, _pointer],
     "chess_board_embedding": [_pointer, _int] + [_pointer] * 7 + [_int] * 12 + [_pointer],
     "chess_move_logits": [_pointer] * 9 + [_int] * 6 + [_pointer],
     "chess_lean_answers": [_pointer] * 4 + [_int] * 5 + [_pointer],

@@ -15,7 +15,7 @@ import torch
 from torch import nn
 
 from model import hip_kernels
-from model.fused_blocks import FusedBlock, linear, link_input_mixes, template_attention, tile_for, transposed_weight
+from model.fused_blocks import FusedBlock, linear, link_input_mixes, template_attention, tile_for
 from model.hip_kernels import aligned, check, library_for, pointer, stream_of
 
 # model/int8_blocks.py:14-17 of the reference: the mlp's hidden is rotated in blocks of 32 (H H^T = 32 I) and
@@ -180,93 +180,6 @@ def _(x, original, residual_scale, input_scale, gain, eps):
     return x.new_empty(x.shape, dtype=torch.float16), x.new_empty(x.shape, dtype=torch.int8), x.new_empty(x.shape[:-1], dtype=torch.float32)
 
 
-# The GEMMs whose output rows norm_quant reads next can normalise them in their own epilogue, one launch for the pair, when
-# a row is NORM_WIDTH outputs (a 64 x 512 tile holds whole rows): the heads' combine with ln2, and down with the following
-# block's ln1. Every output bit is what the two launches give; FUSED_NORMS names the pairs the blocks fuse, from
-# FUSED_NORM_ROWS rows on. None by default: timed on an MI355X in the d512 network, the whole-row tile's fewer, longer
-# workgroups cost what the saved norm_quant launch gains at batch 1024 (22.35 against 22.33 ms a forward with the combine
-# fused, 22.60 with both) and more at batch 64 (3.07 and 3.50 against 2.78 ms).
-NORM_WIDTH = 512
-FUSED_NORMS: set[str] = set()
-FUSED_NORM_ROWS = 0
-
-
-def _norm_outputs(out: torch.Tensor, gain: torch.Tensor, name: str) -> tuple[torch.Tensor, torch.Tensor]:
-    _require(gain, torch.float16, "gain")
-    if out.shape[-1] != NORM_WIDTH or gain.numel() != NORM_WIDTH:
-        raise ValueError(f"{name} normalises rows of {NORM_WIDTH} outputs with as many gains, not {out.shape[-1]} and {gain.numel()}")
-    return torch.empty(out.shape, device=out.device, dtype=torch.int8), torch.empty(out.shape[:-1], device=out.device, dtype=torch.float32)
-
-
-@torch.library.custom_op("chess::linear_norm_quant", mutates_args=())
-def linear_norm_quant(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, residual: torch.Tensor, gain: torch.Tensor,
-                      eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(out, q, scale): out = linear(x, weight, bias, residual=residual) and (q, scale) = norm_quant(out, gain, eps), in one
-    launch, bit for bit the pair the reference runs at int8_blocks.py:282-283 (the heads' combine, then ln2)."""
-    K, N = weight.shape
-    if x.shape[-1] != K:
-        raise ValueError(f"linear_norm_quant: x has {x.shape[-1]} inputs and the weight {K}")
-    for tensor, name in ((x, "x"), (weight, "weight"), (bias, "bias"), (residual, "residual")):
-        _require(tensor, torch.float16, name)
-    library = library_for(x.device)
-    x, residual = aligned(x), aligned(residual)
-    M = x.numel() // K
-    if residual.numel() != M * N:
-        raise ValueError(f"linear_norm_quant: the residual has {residual.numel()} values, not {M} x {N}")
-    out = x.new_empty(*x.shape[:-1], N)
-    q, scale = _norm_outputs(out, gain, "linear_norm_quant")
-    code = library.chess_linear_norm_quant(pointer(x), pointer(aligned(transposed_weight(weight))), pointer(bias.contiguous() if bias is not None else None),
-                                           pointer(residual), pointer(aligned(gain.contiguous())), pointer(out), pointer(q), pointer(scale),
-                                           M, N, K, float(eps), stream_of(x.device))
-    check(code, "linear_norm_quant")
-    return out, q, scale
-
-
-@linear_norm_quant.register_fake
-def _(x, weight, bias, residual, gain, eps):
-    shape = (*x.shape[:-1], weight.shape[1])
-    return x.new_empty(shape), x.new_empty(shape, dtype=torch.int8), x.new_empty(shape[:-1], dtype=torch.float32)
-
-
-@torch.library.custom_op("chess::int8_linear_norm_quant", mutates_args=())
-def int8_linear_norm_quant(x: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, residual: torch.Tensor,
-                           original: torch.Tensor | None, residual_scale: torch.Tensor | None, input_scale: torch.Tensor | None, gain: torch.Tensor,
-                           eps: float) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(out, q, scale): out = int8_linear(x, x_scale, weight, weight_scale, None, residual, False, ..., original, residual_scale,
-    input_scale) and (q, scale) = norm_quant(out, gain, eps), in one launch, bit for bit the reference's down with the following
-    block's input mix (int8_blocks.py:287-288) and that block's norm_quant (:276)."""
-    N, K = weight.shape
-    if K % INT8_DEPTH != 0 or x.shape[-1] != K:
-        raise ValueError(f"int8_linear_norm_quant reads {K} inputs {INT8_DEPTH} at a time, x has {x.shape[-1]}")
-    for tensor, dtype, name in ((x, torch.int8, "x"), (weight, torch.int8, "weight"), (x_scale, torch.float32, "x_scale"),
-                                (weight_scale, torch.float32, "weight_scale"), (residual, torch.float16, "residual"),
-                                (original, torch.float16, "original"), (residual_scale, torch.float16, "residual_scale"),
-                                (input_scale, torch.float16, "input_scale")):
-        _require(tensor, dtype, name)
-    library = library_for(x.device)
-    x, weight, residual, original = aligned(x), aligned(weight), aligned(residual), aligned(original)
-    M = x.numel() // K
-    if x_scale.numel() != M or weight_scale.numel() != N:
-        raise ValueError(f"int8_linear_norm_quant: {x_scale.numel()} row scales for {M} rows, {weight_scale.numel()} weight scales for {N} rows")
-    for tensor, name in ((residual, "residual"), (original, "original")):
-        if tensor is not None and tensor.numel() != M * N:
-            raise ValueError(f"int8_linear_norm_quant: {name} has {tensor.numel()} values, not {M} x {N}")
-    out = torch.empty(*x.shape[:-1], N, device=x.device, dtype=torch.float16)
-    q, scale = _norm_outputs(out, gain, "int8_linear_norm_quant")
-    code = library.chess_int8_linear_norm_quant(pointer(x), pointer(x_scale.contiguous()), pointer(weight), pointer(aligned(weight_scale.contiguous())),
-                                                pointer(residual), pointer(original), pointer(residual_scale), pointer(input_scale),
-                                                pointer(aligned(gain.contiguous())), pointer(out), pointer(q), pointer(scale), M, N, K, float(eps),
-                                                stream_of(x.device))
-    check(code, "int8_linear_norm_quant")
-    return out, q, scale
-
-
-@int8_linear_norm_quant.register_fake
-def _(x, x_scale, weight, weight_scale, residual, original, residual_scale, input_scale, gain, eps):
-    shape = (*x.shape[:-1], weight.shape[0])
-    return x.new_empty(shape, dtype=torch.float16), x.new_empty(shape, dtype=torch.int8), x.new_empty(shape[:-1], dtype=torch.float32)
-
-
 # rotation matrices seen to be Sylvester's H32: the kernel computes that transform by butterflies, never reading them
 _SYLVESTER: dict[tuple[int, int], bool] = {}
 
@@ -327,52 +240,22 @@ class Int8Block(nn.Module):
         #set by link_input_mixes: the next block's scales when down mixes its input, and whether this block's input comes mixed
         self.next_scales: tuple[nn.Parameter, nn.Parameter] | None = None
         self.input_mixed = False
-        #set by link_norm_handoffs: the next block's ln1 (gain, eps) and its slot, when down normalises the next block's input;
-        #handed[0] is (input, q, scale) that the previous block's down left for this block
-        self.next_norm: tuple[nn.Parameter, float, list] | None = None
-        self.handed: list = [None]
 
     def forward(self, x: torch.Tensor, templates: torch.Tensor, original_board_embed: torch.Tensor) -> torch.Tensor:
-        handed, self.handed[0] = self.handed[0], None
-        if self.input_mixed and handed is not None and handed[0] is x:
-            normed, scale = handed[1], handed[2]
-        elif self.input_mixed:
+        if self.input_mixed:
             normed, scale = norm_quant(x, self.ln1.weight, self.ln1.eps)
         else:
             x, normed, scale = mix_norm_quant(x, original_board_embed, self.residual_scale, self.input_scale, self.ln1.weight, self.ln1.eps)
         projected = int8_linear(normed, scale, self.projection, self.projection_scale, self.projection_bias, None, False, "projection")
         attended = template_attention(projected, templates, self.q_gain, self.k_gain, self.heads, self.kv_heads, self.dq, self.dv, self.templates_count,
                                       self.eps)
-        if fuses_norm("combine", self.combine_heads.shape[1], attended.numel() // attended.shape[-1]):
-            x, normed, scale = linear_norm_quant(attended, self.combine_heads, self.combine_heads_bias, x, self.ln2.weight, self.ln2.eps)
-        else:
-            x = linear(attended, self.combine_heads, self.combine_heads_bias, residual=x)
-            normed, scale = norm_quant(x, self.ln2.weight, self.ln2.eps)
+        x = linear(attended, self.combine_heads, self.combine_heads_bias, residual=x)
+        normed, scale = norm_quant(x, self.ln2.weight, self.ln2.eps)
         hidden = int8_linear(normed, scale, self.gate_up, self.gate_up_scale, None, None, True, "gate_up")
         rotated, scale = rotate_quant(hidden, self.hadamard_signs, self.down.shape[1])
         if self.next_scales is None:
             return int8_linear(rotated, scale, self.down, self.down_scale, None, x, False, "down")
-        if self.next_norm is not None and fuses_norm("down", self.down.shape[0], x.numel() // x.shape[-1]):
-            gain, eps, slot = self.next_norm
-            out, normed, scale = int8_linear_norm_quant(rotated, scale, self.down, self.down_scale, x, original_board_embed, *self.next_scales, gain, eps)
-            slot[0] = (out, normed, scale)
-            return out
         return int8_linear(rotated, scale, self.down, self.down_scale, None, x, False, "down", original_board_embed, *self.next_scales)
-
-
-def fuses_norm(pair: str, width: int, rows: int) -> bool:
-    """Whether the block runs pair (combine or down) with the norm_quant after it in one launch."""
-    return pair in FUSED_NORMS and width == NORM_WIDTH and rows >= FUSED_NORM_ROWS
-
-
-def link_norm_handoffs(blocks: list[nn.Module]) -> None:
-    """A down that mixes the next block's input (link_input_mixes) also normalises it with that block's ln1."""
-    for block in blocks:
-        if isinstance(block, Int8Block):
-            block.next_norm, block.handed[0] = None, None
-    for block, following in zip(blocks, blocks[1:]):
-        if isinstance(block, Int8Block) and isinstance(following, Int8Block) and block.next_scales is not None:
-            block.next_norm = (following.ln1.weight, following.ln1.eps, following.handed)
 
 
 def kernels(device: torch.device):
@@ -384,7 +267,6 @@ def quantize_blocks(model: nn.Module, weights: dict[int, dict], output_scale: fl
     """model's blocks of the layers in weights become Int8Blocks; the input mixes are relinked (reference int8_blocks.py:292-298)."""
     blocks = [Int8Block(block, weights[layer], output_scale) if layer in weights else block for layer, block in enumerate(model.encoder)]
     link_input_mixes(blocks)
-    link_norm_handoffs(blocks)
     model.encoder = nn.ModuleList(blocks)
     if weights:
         kernels(next(model.parameters()).device)

@@ -46,9 +46,8 @@ int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int wi
  * epilogue: dequantise by x_scale[M] and w_scale[N(x2)], + bias[N], silu(gate) * up when gated,
  * + residual[M, N], then the next block's input mix when original != NULL; fp16 or bf16 out.
  * K % 64 == 0. tile: 0 picks by size; 1..11 force 64x64, 128x128, 128x64, 256x128, 128x256, 256x64 (rows x
- * outputs), then 128x128, 128x64, 256x64 with a 3-stage ring and 256x64, 128x128 with a 2-stage ring; 12 the
- * persistent gated GEMM (gated, fp16 out, nothing added); 13 128x128 with 128-byte stages (K a multiple of 128
- * bytes). No tile changes a bit.
+ * outputs), then 128x128, 128x64, 256x64 with a 3-stage ring and 256x64, 128x128 with a 2-stage ring; 13 128x128
+ * with 128-byte stages (K a multiple of 128 bytes); 12 is refused. No tile changes a bit.
  * Pointer order of small_int8 (model/int8_cuda.py:35-39); replaces int8_linear_kernel
  * and small_int8 (model/int8_blocks.py:66-144, model/int8_cuda.py:34-183, :362-383). */
 int chess_int8_linear(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* bias, const void* residual,
@@ -78,20 +77,6 @@ int chess_template_attention(const void* projected, const void* keyed_templates,
  * linear (:308-318), whose K x N weight the Python layer transposes once. */
 int chess_linear(const void* x, const void* w, const void* bias, const void* residual, const void* original, const void* residual_scale,
                  const void* input_scale, void* out, int M, int N, int K, int gated, int out_dtype, int tile, void* stream);
-
-/* chess_linear (not gated, fp16 out, residual required) followed by chess_norm_quant of its output, in one launch:
- * out[M, N] as chess_linear writes it, and q[M, N] int8, scale[M] f32 as chess_norm_quant(out, gain, eps) writes
- * them. N == 512 (a 64 x 512 tile holds whole rows). Fuses the pair model/int8_blocks.py:282-283 (the heads'
- * combine linear, then norm_quant with ln2) into one call; the pair's separate entry points stay as they are. */
-int chess_linear_norm_quant(const void* x, const void* w, const void* bias, const void* residual, const void* gain, void* out, void* q,
-                            void* scale, int M, int N, int K, float eps, void* stream);
-
-/* chess_int8_linear (not gated, fp16 out, no bias, residual required, input mix optional) followed by
- * chess_norm_quant of its output, in one launch; N == 512. Fuses model/int8_blocks.py:287-288 (down, with the
- * following block's input mix) and the following block's norm_quant with ln1 (:276) into one call. */
-int chess_int8_linear_norm_quant(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* residual,
-                                 const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* out,
-                                 void* q, void* scale, int M, int N, int K, float eps, void* stream);
 
 /* The network's input out[B, T, D] fp16 from boards[B, T] of token codes (code_bytes 1, 4 or 8 each; 64 <= T <= 128):
  * embed[code] + position[t] (+ the 64 squares' 23 feature rows of table, summed in f32 in slot order and rounded to

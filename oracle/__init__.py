@@ -9,7 +9,7 @@ Modules:
   int8_ops    -- numpy restatement of the int8 hot-path operators
                  (norm_quant, mix_norm_quant, rotate_quant, int8_linear,
                  template_attention, fp16 linear, Int8Block.forward)
-  model_fp32  -- torch-CPU restatement of the fp32 ChessTransformer forward
-                 (the reference's CPU path) plus the int8 network forward
-                 assembled from int8_ops
+  network     -- the fp32 ChessTransformer forward on the CPU (the
+                 reference's CPU path), the input embedding, the heads, and
+                 the int8 network forward assembled from int8_ops
 """

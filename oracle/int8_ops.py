@@ -285,12 +285,3 @@ def int8_block_forward(x, templates, original, block: dict, input_mixed: bool, n
         return int8_linear(rotated, scale, block["down"], block["down_scale"], residual=x)
     return int8_linear(rotated, scale, block["down"], block["down_scale"], residual=x, original=original,
                        residual_scale=next_scales[0], input_scale=next_scales[1])
-
-
-def quantize_weight_rows(weight: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
-    """Per-output-row symmetric round-to-nearest int8 in float64: GPTQ with a diagonal Hessian
-    (engine/quantization.py:76-99; the reference's tests/test_int8.py:35-41 pins that equality)."""
-    weight = np.asarray(weight, dtype=np.float64)
-    scale = np.maximum(np.abs(weight).max(axis=1), 1e-20) / INT8_MAX
-    integers = np.clip(np.round(weight / scale[:, None]), -INT8_MAX, INT8_MAX).astype(np.int8)
-    return integers, scale.astype(F32)

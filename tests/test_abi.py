@@ -81,14 +81,6 @@ def test_refused_shapes_come_back_as_codes(library):
     assert moves(2, 70, 512, 33, 5, 1968) == hip_kernels.INVALID_SHAPE    # more narrow columns than a block
     assert moves(2, 70, 512, 21, 0, 1968) == hip_kernels.INVALID_SHAPE    # board_down's inputs from column 0
     assert library.chess_move_logits(MISALIGNED, 16, 16, 16, 16, 16, 16, 16, 16, 2, 70, 512, 21, 5, 1968, None) == hip_kernels.MISALIGNED
-    # the normalising GEMMs: rows of 512 only, residual and the norm's operands required, 16-byte aligned gain and q
-    assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 4, 256, 64, 1e-5, None) == hip_kernels.UNSUPPORTED
-    assert b"512" in library.chess_last_error()
-    assert library.chess_linear_norm_quant(16, 16, None, None, 16, 16, 16, 16, 4, 512, 64, 1e-5, None) == hip_kernels.INVALID_SHAPE
-    assert library.chess_linear_norm_quant(16, 16, None, 16, MISALIGNED, 16, 16, 16, 4, 512, 64, 1e-5, None) == hip_kernels.MISALIGNED
-    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 4, 512, 100, 1e-5, None) == hip_kernels.INVALID_SHAPE
-    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, 16, None, None, 16, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
-    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, None, 16, 16, 16, 4, 512, 128, 1e-5, None) == hip_kernels.INVALID_SHAPE
     # the lean answers: the indices inside the row, even rows and places, every pointer
     assert library.chess_lean_answers(16, 16, 16, 16, 4, 1968, 508, 70, 220, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_lean_answers(16, 16, 16, 16, 4, 0, 508, 70, 219, None) == hip_kernels.INVALID_SHAPE
@@ -103,8 +95,6 @@ def test_empty_batches_launch_nothing(library):
     assert library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, 0, 70, 512, 21, 5, 1968, None) == 0
     assert library.chess_lean_answers(16, 16, 16, 16, 0, 1968, 508, 70, 219, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
-    assert library.chess_linear_norm_quant(16, 16, None, 16, 16, 16, 16, 16, 0, 512, 64, 1e-5, None) == 0
-    assert library.chess_int8_linear_norm_quant(16, 16, 16, 16, 16, None, None, None, 16, 16, 16, 16, 0, 512, 128, 1e-5, None) == 0
 
 
 def test_codes_become_value_errors_with_the_message(library):

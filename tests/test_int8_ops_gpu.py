@@ -13,8 +13,8 @@ import torch.nn.functional as F
 
 from oracle import int8_ops as oracle
 from model import fused_blocks, int8_blocks
-from model.int8_blocks import (HADAMARD_BLOCK, INT8_TILES, hadamard, int8_linear, int8_linear_norm_quant, int8_matmul_i32, launch_int8_linear,
-                               linear_norm_quant, mix_norm_quant, norm_quant, rotate_quant)
+from model.int8_blocks import (HADAMARD_BLOCK, INT8_TILES, hadamard, int8_linear, int8_matmul_i32, launch_int8_linear, mix_norm_quant, norm_quant,
+                               rotate_quant)
 from model.fused_blocks import launch_linear, launch_template_attention, linear, mix_rms_norm, rms_norm, template_attention
 
 pytestmark = pytest.mark.gpu
@@ -181,83 +181,10 @@ def test_the_gated_epilogue_is_silu_times_up(device, rows):
         assert torch.equal(out, first)
 
 
-@pytest.mark.parametrize("rows, width", [(70, 128), (1000, 2048), (4096, 2048), (71680, 2048)])
-def test_the_streamed_gated_gemm_gives_the_tiled_kernels_bits(device, rows, width):
-    """Tile 12, the persistent gated GEMM: a partial last row block (1000), an even and an odd count of tiles a
-    workgroup (4096, 71680 rows: 2 and 35), the network's batch-1024 shape (71680 x 2048 from 512)."""
-    operands = int8_operands("gate_up", rows, device, width=width, depth=512)
-    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
-    tiled = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 2)
-    streamed = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)
-    assert torch.equal(streamed, tiled)
-    if rows * width <= 70 * 128:
-        expected = oracle_int8_linear(operands).astype(np.float64)
-        assert np.allclose(cpu(streamed).astype(np.float64), expected, atol=1e-3, rtol=2e-3)
-
-
-def test_the_streamed_gated_gemm_refuses_what_it_cannot_take(device):
-    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("gate_up", 70, device, width=200, depth=512)
-    with pytest.raises(ValueError):
-        launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)   # N not a multiple of 64
-    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("projection", 70, device, width=128, depth=512)
-    with pytest.raises(ValueError):
-        launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 12)   # not gated
-
-
 def same_bits(found: torch.Tensor, expected: torch.Tensor) -> bool:
     as_integers = {torch.float16: torch.int16, torch.float32: torch.int32}
     return found.shape == expected.shape and found.dtype == expected.dtype and torch.equal(
         found.view(as_integers.get(found.dtype, found.dtype)), expected.view(as_integers.get(expected.dtype, expected.dtype)))
-
-
-@pytest.mark.parametrize("rows", [70, 1000, 4480, 71680])
-@pytest.mark.parametrize("bias", [True, False])
-def test_linear_norm_quant_gives_the_pairs_bits(device, rows, bias):
-    """The heads' combine and ln2's norm_quant in one launch (the reference's pair int8_blocks.py:282-283): its fp16 rows,
-    q and scale are the two launches' bits; partial last tiles (70, 1000 rows), the batch-64 and batch-1024 shapes."""
-    torch.manual_seed(rows)
-    x = torch.randn(rows, 512, device=device).half()
-    weight = (torch.randn(512, 512, device=device) / math.sqrt(512)).half()
-    b = torch.randn(512, device=device).half() if bias else None
-    residual = (torch.randn(rows, 512, device=device) * 2).half()
-    gain = (torch.rand(512, device=device) + 0.5).half()
-    out, q, scale = linear_norm_quant(x, weight, b, residual, gain, 1e-5)
-    expected = linear(x, weight, b, residual=residual)
-    expected_q, expected_scale = norm_quant(expected, gain, 1e-5)
-    assert same_bits(out, expected) and same_bits(q, expected_q) and same_bits(scale, expected_scale)
-    if rows == 70:
-        want_q, want_scale = oracle.norm_quant(cpu(out), cpu(gain), 1e-5)
-        assert bits_equal(q, want_q) and bits_equal(scale, want_scale)
-
-
-@pytest.mark.parametrize("rows", [70, 210, 4480, 71680])
-@pytest.mark.parametrize("matmul", ["down", "mixing down"])
-def test_int8_linear_norm_quant_gives_the_pairs_bits(device, rows, matmul):
-    """down (with the following block's input mix) and that block's ln1 norm_quant in one launch (the reference's
-    int8_blocks.py:287-288 and :276): the oracle's bits where it is quick, the two launches' bits at every size."""
-    operands = int8_operands(matmul, rows, device, width=512, depth=2048)
-    x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
-    gain = (torch.rand(512, device=device) + 0.5).half()
-    out, q, scale = int8_linear_norm_quant(x, x_scale, weight, weight_scale, residual, *mix, gain, 1e-5)
-    expected = launch_int8_linear(x, x_scale, weight, weight_scale, None, residual, False, *mix, 0)
-    expected_q, expected_scale = norm_quant(expected, gain, 1e-5)
-    assert same_bits(out, expected) and same_bits(q, expected_q) and same_bits(scale, expected_scale)
-    if rows <= 210:
-        want = oracle_int8_linear(operands)
-        want_q, want_scale = oracle.norm_quant(want, cpu(gain), 1e-5)
-        assert bits_equal(out, want) and bits_equal(q, want_q) and bits_equal(scale, want_scale)
-
-
-def test_the_normalising_gemms_refuse_what_they_cannot_take(device):
-    x = torch.randn(70, 512, device=device).half()
-    gain = torch.ones(512, device=device).half()
-    with pytest.raises(ValueError):
-        linear_norm_quant(x, torch.randn(512, 256, device=device).half(), None, torch.randn(70, 256, device=device).half(), gain, 1e-5)  # not 512 wide
-    with pytest.raises(ValueError):
-        linear_norm_quant(x, torch.randn(512, 512, device=device).half(), None, torch.randn(70, 512, device=device).half(), gain[:256], 1e-5)
-    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("down", 70, device, width=256, depth=512)
-    with pytest.raises(ValueError):
-        int8_linear_norm_quant(x, x_scale, weight, weight_scale, residual, *mix, torch.ones(256, device=device).half(), 1e-5)
 
 
 def dequantised(integers: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:

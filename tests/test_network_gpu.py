@@ -119,29 +119,6 @@ def test_down_mixes_the_next_blocks_input_to_the_bit(device):
     assert linked == [False, True] and torch.equal(mixed_in_down, mixed_by_each)
 
 
-def test_the_normalising_gemms_change_no_answer(device, monkeypatch):
-    """The combine and down launches that also normalise their rows (one launch for a GEMM and the norm_quant after it)
-    give the separate launches' answers to the bit, down handing the next block its input's q and scale."""
-    network = int8_network(make_model(FULL, seed=7).to(device), nearest_int8_weights(make_model(FULL, seed=7)))
-    monkeypatch.setattr(int8_blocks, "FUSED_NORMS", {"combine", "down"})
-    calls = {"combine": 0, "down": 0}
-    for name, pair in (("linear_norm_quant", "combine"), ("int8_linear_norm_quant", "down")):
-        def counted(*args, op=getattr(int8_blocks, name), pair=pair):
-            calls[pair] += 1
-            return op(*args)
-        monkeypatch.setattr(int8_blocks, name, counted)
-    blocks = list(network.encoder)
-    int8_count = sum(isinstance(block, Int8Block) for block in blocks)
-    linked = sum(isinstance(block, Int8Block) and isinstance(following, Int8Block) for block, following in zip(blocks, blocks[1:]))
-    boards = random_boards(3, seed=7).to(device)
-    with torch.no_grad():
-        fused = answer_rows(network(boards))
-        monkeypatch.setattr(int8_blocks, "FUSED_NORMS", set())
-        separate = answer_rows(network(boards))
-    assert int8_count > 1 and calls == {"combine": int8_count, "down": linked}
-    assert torch.equal(fused, separate)
-
-
 @pytest.mark.parametrize("settings", [SMALL, FULL])
 def test_the_move_logits_are_the_heads_torch_ops(device, settings):
     """The policy head's launch against the torch ops it replaces (reference fused_blocks.py:866-871), in float64: the

@@ -166,6 +166,27 @@ def test_linear_is_the_matmul():
     assert oracle.linear(x, w, accumulate_fp32=True).dtype == np.float32
 
 
+def test_linears_input_mix_rounds_the_stream_then_weighs_it():
+    """The mix branch of linear (the reference's linear_epilogue MIX, fused_blocks.py:221-224: the stream rounded to the
+    output type, then residual_scale * stream + input_scale * original) through cases that fix its answer exactly: with
+    the input scale 0 it is the unmixed output, with the residual scale 0 the original itself, and with scales 1 and -1
+    and the original set to the rounded stream it is exactly 0, which fails a dropped term, swapped scales, a wrong sign
+    or a stream mixed before its rounding."""
+    x = RNG.standard_normal((30, 64)).astype(np.float16)
+    w = (RNG.standard_normal((64, 48)) / 8).astype(np.float16)
+    residual, original = RNG.standard_normal((30, 48)).astype(np.float16), RNG.standard_normal((30, 48)).astype(np.float16)
+    one, zero = np.float16(1), np.float16(0)
+    stream = oracle.linear(x, w, residual=residual)
+    assert np.array_equal(oracle.linear(x, w, residual=residual, original=original, residual_scale=one, input_scale=zero), stream)
+    assert np.array_equal(oracle.linear(x, w, residual=residual, original=original, residual_scale=zero, input_scale=one), original)
+    unrounded = torch.from_numpy(x).double() @ torch.from_numpy(w).double() + torch.from_numpy(residual).double()
+    assert (unrounded.numpy() != stream.astype(np.float64)).mean() > 0.9     # the rounding is there to be seen
+    cancelled = oracle.linear(x, w, residual=residual, original=stream, residual_scale=one, input_scale=np.float16(-1))
+    assert not cancelled.any()
+    halves = oracle.linear(x, w, residual=residual, original=stream, residual_scale=np.float16(0.5), input_scale=np.float16(0.5))
+    assert np.array_equal(halves, stream)
+
+
 # white to move, so the board is not mirrored: 4k3/3p4/8/3q4/8/2N5/4P3/R3K3 w - - 0 1 (reference tests/test_model.py:166-186)
 KNOWN = [0] * 64
 for _square, _code in {60: 12, 51: 7, 35: 11, 18: 2, 12: 1, 0: 4, 4: 6}.items():
