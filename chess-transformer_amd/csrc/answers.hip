@@ -2,40 +2,36 @@
 // A board's row in a lean lane's input is its tokens, then little-endian int16 indices into the board's answer row,
 // which is the move logits followed by the expected score (engine/inference.py:19-23); a board with fewer legal moves
 // than index slots pads with the expected score's index (engine/selfplay_rs/src/lib.rs:331-333, 540).
-// The reference concatenates the whole answer row (torch.cat) and then gathers from it (torch.gather); this kernel
-// gathers straight from the move logits and the scores, so no B x (moves + 1) answer rows are written and read back.
-// Byte work: one thread an answer, the indices read coalesced along a row, one f32 read and one f32 write each.
+// The heads write the answer rows in place (B x width f32, width = moves + 1); this kernel gathers a lean lane's
+// columns from them, one thread an answer: the int16 index read along the board's row, one f32 read and one f32 write.
 #include "chess_common.h"
 
 namespace {
 
 constexpr int THREADS = 256;
 
-// answers[b][j] = index < moves ? logits[b][index] : score[b], index = the row's int16 at columns_at + 2j. An index
-// outside [0, moves] (which torch's gather stops the device for) gives NaN.
-__global__ __launch_bounds__(THREADS) void lean_answers_kernel(const float* __restrict__ logits, const float* __restrict__ score,
-                                                               const uint8_t* __restrict__ rows, float* __restrict__ answers, int B,
-                                                               int moves, int row_bytes, int columns_at, int columns)
+// answers[b][j] = answer_rows[b][index], index = the row's int16 at columns_at + 2j. An index outside [0, width)
+// (which torch's gather stops the device for) gives NaN.
+__global__ __launch_bounds__(THREADS) void lean_answers_kernel(const float* __restrict__ answer_rows, const uint8_t* __restrict__ rows,
+                                                               float* __restrict__ answers, int B, int width, int row_bytes, int columns_at,
+                                                               int columns)
 {
     const long long at = (long long)blockIdx.x * THREADS + threadIdx.x;
     if (at >= (long long)B * columns) return;
     const int b = (int)(at / columns), j = (int)(at - (long long)b * columns);
     const int index = *reinterpret_cast<const int16_t*>(rows + (size_t)b * row_bytes + columns_at + 2 * j);
-    float value = __builtin_nanf("");
-    if (index >= 0 && index < moves) value = logits[(size_t)b * moves + index];
-    else if (index == moves) value = score[b];
-    answers[at] = value;
+    answers[at] = index >= 0 && index < width ? answer_rows[(size_t)b * width + index] : __builtin_nanf("");
 }
 
 }  // namespace
 
-extern "C" int chess_lean_answers(const void* logits, const void* score, const void* rows, void* answers, int B, int moves, int row_bytes,
-                                  int columns_at, int columns, void* stream)
+extern "C" int chess_lean_answers(const void* answer_rows, const void* rows, void* answers, int B, int width, int row_bytes, int columns_at,
+                                  int columns, void* stream)
 {
-    if (B < 0 || moves <= 0 || moves > 32767 || columns <= 0 || columns_at < 0 || (long long)columns_at + 2LL * columns > row_bytes)
-        return chess_fail(CHESS_INVALID_SHAPE, "lean_answers: %d boards, %d moves, rows of %d bytes with %d indices at byte %d", B, moves,
+    if (B < 0 || width <= 1 || width > 32768 || columns <= 0 || columns_at < 0 || (long long)columns_at + 2LL * columns > row_bytes)
+        return chess_fail(CHESS_INVALID_SHAPE, "lean_answers: %d boards, answer rows of %d, rows of %d bytes with %d indices at byte %d", B, width,
                           row_bytes, columns, columns_at);
-    if (!logits || !score || !rows || !answers) return chess_fail(CHESS_INVALID_SHAPE, "lean_answers: a required pointer is null");
+    if (!answer_rows || !rows || !answers) return chess_fail(CHESS_INVALID_SHAPE, "lean_answers: a required pointer is null");
     if (((uintptr_t)rows | (uintptr_t)row_bytes | (uintptr_t)columns_at) & 1u)
         return chess_fail(CHESS_MISALIGNED, "lean_answers reads int16 indices: the rows, their length and the indices' place must be even");
     if (B == 0) return CHESS_OK;
@@ -43,7 +39,6 @@ extern "C" int chess_lean_answers(const void* logits, const void* score, const v
     if ((total + THREADS - 1) / THREADS > 0x7fffffffLL)
         return chess_fail(CHESS_UNSUPPORTED, "lean_answers: %lld answers are more than one launch takes", total);
     hipLaunchKernelGGL(lean_answers_kernel, dim3((unsigned)((total + THREADS - 1) / THREADS)), dim3(THREADS), 0, (hipStream_t)stream,
-                       (const float*)logits, (const float*)score, (const uint8_t*)rows, (float*)answers, B, moves, row_bytes, columns_at,
-                       columns);
+                       (const float*)answer_rows, (const uint8_t*)rows, (float*)answers, B, width, row_bytes, columns_at, columns);
     return launch_status();
 }

@@ -1,0 +1,33 @@
+// Declarations shared by the GEMM's translation units: the epilogue's operands and flags, and one dispatcher per
+// operand and output type (each built in a translation unit of its own, so that the library's tiles compile in parallel).
+#pragma once
+
+#include "chess_common.h"
+
+namespace gemm {
+
+constexpr int STAGE_K_BYTES = 64;
+constexpr int TILES = 13;       // tiles 1 to 13 (12 is not one); 0 picks by size
+
+enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4 };
+
+struct Epilogue {
+    const float* x_scale;        // int8 only
+    const float* w_scale;        // int8 only
+    const half_t* bias;
+    const half_t* residual;
+    const half_t* original;
+    const half_t* residual_scale;
+    const half_t* input_scale;
+    int flags;
+};
+
+// dispatch(In, NB, OutT): tile 0 picks by size; gated takes the gate's and up's weight rows (NB = 2)
+int dispatch_i8_f16(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream);
+int dispatch_i8_bf16(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream);
+int dispatch_i8_gated(int out_dtype, const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream);
+int dispatch_i8_i32(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream);
+int dispatch_f16(int gated, int out_dtype, const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile,
+                 hipStream_t stream);
+
+}  // namespace gemm

@@ -1,0 +1,517 @@
+// The network's GEMMs on CDNA4 MFMA, with their fused epilogues:
+//   int8: out[M, N] = epilogue(x[M, K] @ w[N, K]^T), x and w int8, exact int32 sums (v_mfma_i32_32x32x32_i8);
+//         what model/int8_blocks.py:66-144 (int8_linear_kernel) and model/int8_cuda.py:34-183 (small_int8) compute.
+//   fp16: out[M, N] = epilogue(x[M, K] @ W[K, N]), x and W fp16, f32 sums (v_mfma_f32_32x32x16_f16); what
+//         model/fused_blocks.py:229-304 (linear_kernel) computes, W taken transposed as w = W^T [N, K].
+// int8 epilogue op order (f32, one IEEE op per step, no fma):
+//   v = f32(acc) * x_scale[m];  out = v * w_scale[n]
+//   [BIAS]      out = out + bias[n]
+//   [GATED]     up = (f32(acc_up) * x_scale[m]) * w_scale[N + n];  out = silu(out) * up
+//   [RESIDUAL]  out = out + residual[m, n]
+//   [MIX]       out = (f32(round(out)) * residual_scale) + (original[m, n] * input_scale)
+//   round to fp16 / bf16 (or, for the accumulator entry point, the raw int32 sums).
+// The fp16 epilogue is the same from the f32 sums, without the scales. The int32 sums are exact in any
+// order, and every tile shape runs the same epilogue, so the tile chosen for a shape never changes a bit.
+//
+// Layout: x row-major [M, K], w row-major [N(x2 gated), K] (the gate's rows, then up's); a stage is 64 bytes
+// of K (64 int8 or 32 fp16 elements), and K must be a multiple of it.
+// A workgroup of 4 wavefronts takes a BM x BN tile of outputs (gated: BN outputs from 2 BN weight rows);
+// the wavefronts split it WAVES_M x WAVES_N into 32 x 32 MFMA fragments.
+//
+// K advances a stage at a time through a ring of STAGES stages in LDS, filled by the DMA loads
+// global_load_lds_dwordx4 (global memory straight to LDS, no registers): STAGES - 1 stages are in flight
+// while one is multiplied, and a wavefront waits (s_waitcnt vmcnt) only for the stage it is about to read.
+// A stage holds 1 KB blocks of 16 rows x 64 bytes, a DMA instruction's 64 lanes each writing 16 bytes at
+// 16 x lane. Lanes 4 r .. 4 r + 3 read row r's 64 bytes, so neighbouring lanes read neighbouring bytes (the
+// load path is 3x slower when they are a row apart); lane 4 r + j takes chunk j ^ (r / 4), an XOR swizzle
+// under which the 16 rows an MFMA operand group reads sit in 16 different 16-byte LDS bank groups.
+// An MFMA operand lane holds 16 consecutive bytes of one row (16 int8 or 8 fp16); which k a byte stands
+// for is the same for both operands, so the sums are the dot products whatever the hardware's k order. The
+// weights are the MFMA's first operand: a lane's results are then groups of 4 consecutive columns of one
+// row, which take their column scales and bias 16 bytes at a time.
+// The epilogue runs in two phases through LDS: the dequantised (and gated) f32 tile is staged, then read
+// back by rows, so that residual, input embedding and outputs move 16 bytes a lane with a row's columns
+// contiguous across lanes.
+#pragma once
+
+#include "gemm.h"
+#include "lds_dma.h"
+
+#include <type_traits>
+
+namespace {
+
+using namespace gemm;
+constexpr int THREADS = 256;
+constexpr int BLOCK = 1024;      // bytes a DMA instruction writes: 16 rows x 64 bytes
+
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+template <typename In> struct Mfma;
+template <> struct Mfma<int8_t> {
+    typedef v16i Acc;
+    typedef v4i Operand;
+    static DEVICE Acc step(Operand a, Operand b, Acc c) { return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0); }
+    static DEVICE float value(Acc c, int r) { return (float)c[r]; }
+};
+template <> struct Mfma<half_t> {
+    typedef v16f Acc;
+    typedef v8h Operand;
+    static DEVICE Acc step(Operand a, Operand b, Acc c) { return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0); }
+    static DEVICE float value(Acc c, int r) { return c[r]; }
+};
+
+// outputs are streamed (non-temporal stores), so that they do not push the operands out of L2
+template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
+template <> DEVICE void store_eight<half_t>(half_t* to, const float (&v)[8]) {
+    const v8h eight = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+    __builtin_nontemporal_store(eight, reinterpret_cast<v8h*>(to));
+}
+template <> DEVICE void store_eight<bf16_t>(bf16_t* to, const float (&v)[8]) {
+    v4u packed;
+#pragma unroll
+    for (int c = 0; c < 4; c++) packed[c] = (uint32_t)bf16_from_float(v[2 * c]).bits | ((uint32_t)bf16_from_float(v[2 * c + 1]).bits << 16);
+    __builtin_nontemporal_store(packed, reinterpret_cast<v4u*>(to));
+}
+template <> DEVICE void store_eight<float>(float* to, const float (&v)[8]) {
+    __builtin_nontemporal_store(v4f{v[0], v[1], v[2], v[3]}, reinterpret_cast<v4f*>(to));
+    __builtin_nontemporal_store(v4f{v[4], v[5], v[6], v[7]}, reinterpret_cast<v4f*>(to + 4));
+}
+
+template <typename OutT> DEVICE void stage_four(OutT* to, const float (&v)[4]);
+template <> DEVICE void stage_four<half_t>(half_t* to, const float (&v)[4]) {
+    *reinterpret_cast<v4h*>(to) = v4h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+template <> DEVICE void stage_four<bf16_t>(bf16_t* to, const float (&v)[4]) {
+    const uint32_t lo = (uint32_t)bf16_from_float(v[0]).bits | ((uint32_t)bf16_from_float(v[1]).bits << 16);
+    const uint32_t hi = (uint32_t)bf16_from_float(v[2]).bits | ((uint32_t)bf16_from_float(v[3]).bits << 16);
+    *reinterpret_cast<uint2*>(to) = uint2{lo, hi};
+}
+template <typename OutT> DEVICE void stage_four(OutT*, const float (&)[4]) {}
+
+// A stage is SK bytes of K: 64 (16 rows a 1 KB block, 4 lanes a row) or 128 (8 rows a block, 8 lanes a row, so that a
+// DMA instruction reads whole 128-byte lines: the L2 serves 128-byte lines, and with 64-byte stages each line of an
+// operand row is read twice, a step apart). A lane's 16-byte chunk of a row sits at chunk ^ swizzle(row) of its row's
+// slots: over the 16 rows an MFMA operand group reads, the chunks fall in 16 different 16-byte bank groups.
+template <int SK> constexpr int block_rows() { return BLOCK / SK; }
+template <int SK> DEVICE int chunk_swizzle(int row) { return SK == 64 ? (row & 15) >> 2 : (row & 15) >> 1; }
+
+// An f32 staged tile (an epilogue that still adds to it) is staged half its rows at a time when every wavefront
+// has two or more row fragments: half the LDS, so that more workgroups fit a CU.
+template <int BM, int WAVES_M, bool PACKED> constexpr int staging_halves() { return !PACKED && (BM / WAVES_M / 32) % 2 == 0 ? 2 : 1; }
+
+// LDS: the ring of stages, reused after the main loop for the staged output tile; then the epilogue's column
+// and row vectors (f32: NB x BN weight scales and BM row scales for int8, BN bias)
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED, int SK = 64>
+constexpr int vector_offset() {
+    constexpr int RING = STAGES * (BM / block_rows<SK>() + NB * BN / block_rows<SK>()) * BLOCK;
+    constexpr int STAGING = PACKED ? BM * (BN + 8) * 2 : BM / staging_halves<BM, WAVES_M, PACKED>() * (BN + 4) * 4;
+    return RING > STAGING ? RING : STAGING;
+}
+template <typename In, int BM, int BN, int WAVES_M, int NB, int STAGES, typename OutT, bool PACKED, int SK = 64>
+constexpr int lds_bytes() {
+    constexpr bool SCALED = std::is_same<In, int8_t>::value && !std::is_same<OutT, int>::value;
+    return vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>() + ((SCALED ? NB * BN + BM : 0) + BN) * 4;
+}
+
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI, int SK = 64>
+__global__ __launch_bounds__(THREADS) void gemm_kernel(
+    const In* __restrict__ x, const In* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
+{
+    static_assert(WAVES_M * WAVES_N * 64 == THREADS, "four wavefronts");
+    typedef Mfma<In> MMA;
+    constexpr bool INT8 = std::is_same<In, int8_t>::value;
+    constexpr bool RAW = std::is_same<OutT, int>::value;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N, FM = WM / 32, FN = WN / 32;
+    constexpr int ROWS_A_BLOCK = block_rows<SK>(), CHUNKS = SK / 16, SUBS = SK / 32;
+    constexpr int A_BLOCKS = BM / ROWS_A_BLOCK, B_BLOCKS = NB * BN / ROWS_A_BLOCK, BLOCKS = A_BLOCKS + B_BLOCKS;
+    constexpr int PER_WAVE = BLOCKS / 4;
+    constexpr int STAGE_BYTES = BLOCKS * BLOCK;
+    static_assert(SK == 64 || SK == 128, "stages of 64 or 128 bytes");
+    static_assert(BLOCKS % 4 == 0 && FM >= 1 && FN >= 1, "tile shape");
+    extern __shared__ __align__(16) int8_t lds[];
+
+    // the wavefront as a scalar (the compiler takes tid / 64 for a per-lane value): block indices, LDS destinations
+    // and the branches on them stay scalar
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    // the epilogue's flags: fixed by the instantiation (EPI >= 0, the network's combinations), else read at run time
+    const int flags = EPI >= 0 ? EPI : e.flags;
+    const size_t row_bytes = (size_t)K * sizeof(In);
+    const int steps = (int)(row_bytes / SK);
+
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int tile = xcd_local_tile(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GROUP_M = 8;
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = tile / in_group * GROUP_M;
+    const int group_rows = min(tiles_m - first_m, GROUP_M);
+    const int m0 = (first_m + tile % in_group % group_rows) * BM;
+    const int n0 = (tile % in_group / group_rows) * BN;
+
+    // this lane's source in each of the wavefront's blocks: row lane / CHUNKS of the block, 16-byte chunk
+    // (lane % CHUNKS) ^ swizzle(row). Rows past M read row M - 1 and columns past N read column N - 1: their sums are
+    // never stored.
+    // A block's source is a scalar base (x or w, the block index being the same in all lanes) plus a 32-bit lane
+    // offset, so that the step's loads take the scalar-base form with no per-step address arithmetic in the lanes.
+    uint32_t source[PER_WAVE];
+#pragma unroll
+    for (int p = 0; p < PER_WAVE; p++) {
+        const int block = wave * PER_WAVE + p;
+        const int row = (block < A_BLOCKS ? block : block - A_BLOCKS) * ROWS_A_BLOCK + lane / CHUNKS;
+        const int chunk = ((lane % CHUNKS) ^ chunk_swizzle<SK>(row)) * 16;
+        if (block < A_BLOCKS) {
+            source[p] = (uint32_t)min(m0 + row, M - 1) * (uint32_t)row_bytes + chunk;
+        } else {
+            const int group = row / BN, col = min(n0 + row % BN, N - 1);
+            source[p] = (uint32_t)(group * N + col) * (uint32_t)row_bytes + chunk;
+        }
+    }
+    // The epilogue's operands are loaded now, so that they arrive while the main loop runs instead of after it:
+    // the tile's column vectors (weight scales of the NB row groups, bias) and row scales, parked in LDS after
+    // the loop, and the residual / original rows of phase 2, kept in registers. Past-the-edge places read
+    // the last row / column (never stored).
+    constexpr bool SCALED = INT8 && !RAW;
+    constexpr int VEC_XS = SCALED ? NB * BN : 0, VEC_BIAS = VEC_XS + (SCALED ? BM : 0), VEC = RAW ? 0 : VEC_BIAS + BN;
+    constexpr int VEC_PER_THREAD = (VEC + THREADS - 1) / THREADS;
+    // One unconditional 32-bit load a slot, from a chosen address (a bias half comes in the aligned word that holds
+    // it), kept as raw bits: loads under divergent branches, or converted as they arrive, would be waited for here.
+    uint32_t vec[VEC_PER_THREAD > 0 ? VEC_PER_THREAD : 1];
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++) {
+        const int at = tid + v * THREADS;
+        const uint32_t* from = (const uint32_t*)x;   // any readable word, for slots that hold nothing
+        if (at < VEC_XS) {
+            from = (const uint32_t*)(e.w_scale + (size_t)(at / BN) * N + min(n0 + at % BN, N - 1));
+        } else if (at < VEC_BIAS) {
+            from = (const uint32_t*)(e.x_scale + min(m0 + at - VEC_XS, M - 1));
+        } else if (at < VEC && (flags & EPI_BIAS)) {
+            from = (const uint32_t*)e.bias + min(n0 + at - VEC_BIAS, N - 1) / 2;
+        }
+        vec[v] = *from;
+    }
+    uint16_t mix_scales[2] = {0, 0};
+    if (!RAW && (flags & EPI_MIX)) {
+        mix_scales[0] = __builtin_bit_cast(uint16_t, e.residual_scale[0]);
+        mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
+    }
+    constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = BM / ROWS;
+    // Staged in halves, half h holds row fragments h * HALF_FM .. of every wavefront: staged row r is tile row
+    // (r / HALF_ROWS) * WM + h * HALF_ROWS + r % HALF_ROWS.
+    constexpr int HALVES = staging_halves<BM, WAVES_M, PACKED>(), HALF_FM = FM / HALVES, HALF_ROWS = WM / HALVES;
+    constexpr int HALF_PASSES = PASSES / HALVES;
+    static_assert(PASSES % HALVES == 0, "passes split between the halves");
+    auto pass_row = [&](int pass) {   // the tile row a lane takes in phase 2's pass
+        const int staged_row = pass % HALF_PASSES * ROWS + tid / ROW_LANES;
+        return HALVES == 1 ? staged_row : staged_row / HALF_ROWS * WM + pass / HALF_PASSES * HALF_ROWS + staged_row % HALF_ROWS;
+    };
+    constexpr bool ADDS = !RAW && !PACKED;   // phase 2 may add the residual and mix in the original
+    // The residual / original rows of phase 2, held in registers: all of them loaded now while they fit beside the sums
+    // (8 passes, 64 registers at most). A pass's own loads would wait: they cannot move above the previous pass's stores,
+    // which the compiler cannot tell apart from them. (Tiles of more than 8 passes read in phase 2: with held rows the
+    // compiler fails on the gated 256 x 128 tile.)
+    constexpr bool HELD = ADDS && PASSES <= 8;
+    const bool vectors = N % 8 == 0;
+    v8h residual_rows[HELD ? PASSES : 1], original_rows[HELD ? PASSES : 1];
+    auto load_rows = [&](int pass) {
+        const size_t at = (size_t)min(m0 + pass_row(pass), M - 1) * N + min(n0 + (tid % ROW_LANES) * 8, N - 8);
+        if (vectors && (flags & EPI_RESIDUAL)) residual_rows[pass] = *reinterpret_cast<const v8h*>(e.residual + at);
+        if (vectors && (flags & EPI_MIX)) original_rows[pass] = *reinterpret_cast<const v8h*>(e.original + at);
+    };
+    if constexpr (HELD) {
+#pragma unroll
+        for (int pass = 0; pass < PASSES; pass++) load_rows(pass);
+    }
+
+    LDS_SPACE int8_t* ring = (LDS_SPACE int8_t*)lds;
+    // The operands as buffer resources: a DMA load takes the lane's offset from a VGPR and the step's K offset from an
+    // SGPR, with no address arithmetic in the lanes. (The host keeps both operands under 4 GiB.)
+    const BufferResource x_rsrc = buffer_resource(x, (uint32_t)M * (uint32_t)row_bytes);
+    const BufferResource w_rsrc = buffer_resource(w, (uint32_t)NB * (uint32_t)N * (uint32_t)row_bytes);
+    // the DMA of step into ring stage S (S == step % STAGES, fixed at compile time)
+    auto issue = [&](int step, auto stage_index) {
+        constexpr int S = decltype(stage_index)::value;
+        const int k0 = min(step, steps - 1) * SK;
+#pragma unroll
+        for (int p = 0; p < PER_WAVE; p++)
+            buffer_dma16(wave * PER_WAVE + p < A_BLOCKS ? x_rsrc : w_rsrc, (LDS_SPACE void*)(ring + S * STAGE_BYTES + (wave * PER_WAVE + p) * BLOCK),
+                         source[p], k0);
+    };
+
+    typename MMA::Acc acc[NB][FM][FN];
+
+    // an operand lane (row lane % 32, 16-byte half lane / 32 of each 32-byte sub-step) in a stage: the block of its
+    // row, then the slot CHUNKS r + (chunk ^ swizzle(r)) of row r's chunk
+    const int in_row = lane & 31, half = lane >> 5;
+    // a lane's operand addresses in stage 0: this wavefront's A rows and B columns (the fragment and stage offsets
+    // are then immediates)
+    int a_operand[SUBS], b_operand[SUBS];
+#pragma unroll
+    for (int sub = 0; sub < SUBS; sub++) {
+        const int operand = (in_row / ROWS_A_BLOCK) * BLOCK
+                          + ((in_row % ROWS_A_BLOCK) * CHUNKS + ((half + 2 * sub) ^ chunk_swizzle<SK>(in_row))) * 16;
+        a_operand[sub] = operand + (wm * WM / ROWS_A_BLOCK) * BLOCK;
+        b_operand[sub] = operand + (A_BLOCKS + wn * WN / ROWS_A_BLOCK) * BLOCK;
+    }
+
+    static_for<0, STAGES - 1>([&](auto s) { issue(decltype(s)::value, s); });
+    // a step's MFMAs; the first step's start from zero sums (the MFMA's zero accumulator operand), so nothing clears them
+    auto multiply = [&](auto stage_index, auto first_step) {
+        constexpr bool FIRST = decltype(first_step)::value;
+        constexpr int STAGE = decltype(stage_index)::value * STAGE_BYTES;
+#pragma unroll
+        for (int sub = 0; sub < SUBS; sub++) {
+            typename MMA::Operand af[FM];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                af[i] = *(const LDS_SPACE typename MMA::Operand*)(ring + a_operand[sub] + STAGE + (i * 32 / ROWS_A_BLOCK) * BLOCK);
+#pragma unroll
+            for (int g = 0; g < NB; g++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    const typename MMA::Operand bf =
+                        *(const LDS_SPACE typename MMA::Operand*)(ring + b_operand[sub] + STAGE + ((g * BN + j * 32) / ROWS_A_BLOCK) * BLOCK);
+#pragma unroll
+                    for (int i = 0; i < FM; i++)
+                        acc[g][i][j] = MMA::step(bf, af[i], FIRST && sub == 0 ? typename MMA::Acc{} : acc[g][i][j]);
+                }
+        }
+    };
+    // a step: its stage landed and the stage it refills read by every wavefront; the DMA STAGES - 1 steps ahead (past
+    // the end it loads the last step again); its MFMAs
+    auto run_step = [&](int step, auto stage_index, auto first_step) {
+        constexpr int S = decltype(stage_index)::value;
+        stage_barrier<PER_WAVE * (STAGES - 2)>();
+        issue(step + STAGES - 1, std::integral_constant<int, (S + STAGES - 1) % STAGES>{});
+        multiply(stage_index, first_step);
+    };
+    // step 0 (its MFMAs start from zero sums), then STAGES steps a turn, so that every stage offset is an immediate
+    run_step(0, std::integral_constant<int, 0>{}, std::true_type{});
+    for (int turn = 1; turn < steps; turn += STAGES) {
+        static_for<0, STAGES>([&](auto s) {
+            if (turn + decltype(s)::value < steps)
+                run_step(turn + decltype(s)::value, std::integral_constant<int, (1 + decltype(s)::value) % STAGES>{}, std::false_type{});
+        });
+    }
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));   // the tail's repeated loads land before the LDS is reused
+    // the prefetched raw bits are first touched here, so that nothing converts (and waits for) them before the loop
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++) asm volatile("" : "+v"(vec[v]));
+    asm volatile("" : "+v"(mix_scales[0]), "+v"(mix_scales[1]));
+    float* vectors_lds = (float*)(lds + vector_offset<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>());
+#pragma unroll
+    for (int v = 0; v < VEC_PER_THREAD; v++)
+        if (const int at = tid + v * THREADS; at < VEC) {
+            const int shift = (min(n0 + at - VEC_BIAS, N - 1) & 1) * 16;   // a bias's half of its word
+            vectors_lds[at] = at < VEC_BIAS ? __uint_as_float(vec[v])
+                                            : (flags & EPI_BIAS) ? (float)__builtin_bit_cast(half_t, (uint16_t)(vec[v] >> shift)) : 0.0f;
+        }
+    __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);
+    bare_barrier();
+
+    // Phase 1, in the MFMA layout: dequantise, bias, SiLU * up, then stage the tile in LDS: in f32 ([BM][BN + 4], or
+    // half the rows at a time, each half then taken by phase 2) when phase 2 still adds to it, else (PACKED) already
+    // rounded to the 16-bit output ([BM][BN + 8]).
+    // A fragment's lane holds row lane % 32 and, in register 4 q + r, column 8 q + 4 (lane / 32) + r.
+    float* staged = (float*)lds;
+    OutT* packed = (OutT*)lds;
+    const float* column = vectors_lds;   // [NB][BN] weight scales, then [BM] row scales, then [BN] bias
+    const float rs = (float)__builtin_bit_cast(half_t, mix_scales[0]), is = (float)__builtin_bit_cast(half_t, mix_scales[1]);
+#pragma unroll
+    for (int h = 0; h < HALVES; h++) {
+        if (h > 0) {
+            __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // the previous half's staged rows are read
+            bare_barrier();
+        }
+#pragma unroll
+        for (int fi = 0; fi < HALF_FM; fi++) {
+            const int i = h * HALF_FM + fi;
+            const int m_local = wm * WM + i * 32 + in_row;
+            const int staged_row = HALVES == 1 ? m_local : wm * HALF_ROWS + fi * 32 + in_row;
+            const float xs = SCALED ? column[VEC_XS + m_local] : 1.0f;
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n_local = wn * WN + j * 32 + 8 * q + 4 * half;
+                    float value[4];
+                    if constexpr (RAW) {
+#pragma unroll
+                        for (int r = 0; r < 4; r++) value[r] = __int_as_float((int)acc[0][i][j][4 * q + r]);
+                    } else {
+                        const float4 ws = SCALED ? *reinterpret_cast<const float4*>(column + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                        const float4 ws_up = SCALED && NB == 2 ? *reinterpret_cast<const float4*>(column + BN + n_local) : float4{1.0f, 1.0f, 1.0f, 1.0f};
+                        const float4 b = *reinterpret_cast<const float4*>(column + VEC_BIAS + n_local);
+                        const float ws_r[4] = {ws.x, ws.y, ws.z, ws.w}, ws_up_r[4] = {ws_up.x, ws_up.y, ws_up.z, ws_up.w}, b_r[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            if constexpr (INT8) {
+                                value[r] = (MMA::value(acc[0][i][j], 4 * q + r) * xs) * ws_r[r];
+                            } else {
+                                value[r] = MMA::value(acc[0][i][j], 4 * q + r);
+                            }
+                            if (flags & EPI_BIAS) value[r] = value[r] + b_r[r];
+                            if constexpr (NB == 2) {
+                                const float up = INT8 ? (MMA::value(acc[1][i][j], 4 * q + r) * xs) * ws_up_r[r] : MMA::value(acc[1][i][j], 4 * q + r);
+                                value[r] = silu_fast(value[r]) * up;
+                            }
+                        }
+                    }
+                    if constexpr (PACKED) {
+                        // the f32 value is what rounds: keep its last multiply out of the conversion (one rounding, not two)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) asm volatile("" : "+v"(value[r]));
+                        stage_four<OutT>(packed + m_local * (BN + 8) + n_local, value);
+                    } else {
+                        *reinterpret_cast<float4*>(staged + staged_row * (BN + 4) + n_local) = float4{value[0], value[1], value[2], value[3]};
+                    }
+                }
+        }
+        __builtin_amdgcn_s_waitcnt(LGKMCNT_ZERO);   // this wavefront's staging writes are done
+        bare_barrier();
+
+        // Phase 2, in rows: 8 consecutive columns a lane, so the residual and the input embedding are read and the
+        // outputs written 16 bytes a lane (32 for f32), a row's columns contiguous across the lanes.
+#pragma unroll
+        for (int hp = 0; hp < HALF_PASSES; hp++) {
+            const int pass = h * HALF_PASSES + hp;
+            const int staged_row = hp * ROWS + tid / ROW_LANES;
+            const int m_local = pass_row(pass), n_local = (tid % ROW_LANES) * 8;
+            const int m = m0 + m_local, n = n0 + n_local;
+            if (m >= M || n >= N) continue;
+            const size_t at = (size_t)m * N + n;
+            if constexpr (PACKED) {
+                const uint4 eight = *reinterpret_cast<const uint4*>(packed + staged_row * (BN + 8) + n_local);
+                if (vectors) {
+                    __builtin_nontemporal_store(__builtin_bit_cast(v4u, eight), reinterpret_cast<v4u*>(out + at));
+                } else {
+                    const OutT* values = reinterpret_cast<const OutT*>(&eight);
+#pragma unroll
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) out[at + c] = values[c];
+                }
+                continue;
+            }
+            const float4 lo = *reinterpret_cast<const float4*>(staged + staged_row * (BN + 4) + n_local);
+            const float4 hi = *reinterpret_cast<const float4*>(staged + staged_row * (BN + 4) + n_local + 4);
+            float value[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+            if constexpr (RAW) {
+                if (vectors) {
+                    *reinterpret_cast<uint4*>(out + at) = uint4{__float_as_uint(value[0]), __float_as_uint(value[1]), __float_as_uint(value[2]), __float_as_uint(value[3])};
+                    *reinterpret_cast<uint4*>(out + at + 4) = uint4{__float_as_uint(value[4]), __float_as_uint(value[5]), __float_as_uint(value[6]), __float_as_uint(value[7])};
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) out[at + c] = __float_as_int(value[c]);
+                }
+            } else {
+                if (flags & EPI_RESIDUAL) {
+                    if (vectors) {
+#pragma unroll
+                        for (int c = 0; c < 8; c++)
+                            value[c] = value[c] + (float)(HELD ? residual_rows[HELD ? pass : 0] : *reinterpret_cast<const v8h*>(e.residual + at))[c];
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; c++)
+                            if (n + c < N) value[c] = value[c] + (float)e.residual[at + c];
+                    }
+                }
+                if (flags & EPI_MIX) {
+                    float original[8];
+                    if (vectors) {
+#pragma unroll
+                        for (int c = 0; c < 8; c++)
+                            original[c] = (float)(HELD ? original_rows[HELD ? pass : 0] : *reinterpret_cast<const v8h*>(e.original + at))[c];
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 8; c++) original[c] = n + c < N ? (float)e.original[at + c] : 0.0f;
+                    }
+#pragma unroll
+                    for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + (original[c] * is);
+                }
+                if (vectors) {
+                    store_eight<OutT>(out + at, value);
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 8; c++)
+                        if (n + c < N) out[at + c] = from_float<OutT>(value[c]);
+                }
+            }
+        }
+    }
+}
+
+template <typename In, int BM, int BN, int WAVES_M, int WAVES_N, int NB, int STAGES, typename OutT, bool PACKED, int EPI, int SK = 64>
+int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
+    if (((size_t)K * sizeof(In)) % SK != 0)
+        return chess_fail(CHESS_UNSUPPORTED, "a tile of %d-byte stages reads rows of a multiple of %d bytes, not %d", SK, SK, (int)(K * sizeof(In)));
+    constexpr int BYTES = lds_bytes<In, BM, BN, WAVES_M, NB, STAGES, OutT, PACKED, SK>();
+    auto kernel = gemm_kernel<In, BM, BN, WAVES_M, WAVES_N, NB, STAGES, OutT, PACKED, EPI, SK>;
+    if (BYTES > 65536) {
+        static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
+        if (allowed != hipSuccess) return (int)allowed;
+    }
+    const int tiles = ((M + BM - 1) / BM) * ((N + BN - 1) / BN);
+    hipLaunchKernelGGL(kernel, dim3(tiles), dim3(THREADS), BYTES, stream, (const In*)x, (const In*)w, (OutT*)out, e, M, N, K);
+    return launch_status();
+}
+
+
+
+// The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
+// 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
+// 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
+// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
+// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2)  13: 128 x 128 (2 x 2, 2) with stages of 128 bytes of K (rows of a
+// multiple of 128 bytes). 0 picks by the launch's size; 12 is not a tile.
+template <typename In, int NB, typename OutT, bool PACKED, int EPI>
+int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    switch (tile) {
+        case 1: return launch<In, 64, 64, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 2: return launch<In, 128, 128, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 3: return launch<In, 128, 64, 2, 2, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 4: return launch<In, 256, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 5: return launch<In, 128, 256, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 6: return launch<In, 256, 64, 4, 1, NB, 4, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 9: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 10: return launch<In, 256, 64, 4, 1, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 13: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);
+        default: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+    }
+}
+
+// The tile for tile 0: large launches take the 2-stage 128 x 128, with 128-byte stages for rows of 2 KB or more that
+// are a multiple of 128 bytes (each L2 line of an operand row read once); smaller ones the 4-stage tiles that still
+// give the chip a workgroup a compute unit.
+template <typename In> int tile_by_size(int M, int N, int K) {
+    const size_t row_bytes = (size_t)K * sizeof(In);
+    if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 512) return row_bytes >= 2048 && row_bytes % 128 == 0 ? 13 : 11;
+    if ((long)((M + 127) / 128) * ((N + 127) / 128) >= 256) return 2;
+    return (long)((M + 127) / 128) * ((N + 63) / 64) >= 128 ? 3 : 1;
+}
+
+// The epilogues the network and the standalone configs use are built with their flags fixed, for fp16 and bf16 outputs
+// alike; any other combination reads them at run time. A 16-bit output with nothing left to add is staged already
+// rounded (half the LDS of the f32 staging).
+template <typename In, int NB, typename OutT>
+int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    if (tile == 0) tile = tile_by_size<In>(M, N, K);
+    if (tile == 12) return chess_fail(CHESS_UNSUPPORTED, "tile 12 is not a tile of this GEMM");
+    const int f = e.flags;
+    if constexpr (sizeof(OutT) == 2) {
+        if (f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);
+        if constexpr (NB == 1) {
+            if (f == EPI_BIAS) return by_tile<In, NB, OutT, true, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);
+            if (f == EPI_RESIDUAL) return by_tile<In, NB, OutT, false, EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+            if (f == (EPI_RESIDUAL | EPI_MIX)) return by_tile<In, NB, OutT, false, EPI_RESIDUAL | EPI_MIX>(x, w, out, e, M, N, K, tile, stream);
+            if (f == (EPI_BIAS | EPI_RESIDUAL)) return by_tile<In, NB, OutT, false, EPI_BIAS | EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+        }
+        if (!(f & (EPI_RESIDUAL | EPI_MIX))) return by_tile<In, NB, OutT, true, -1>(x, w, out, e, M, N, K, tile, stream);
+    }
+    return by_tile<In, NB, OutT, false, -1>(x, w, out, e, M, N, K, tile, stream);
+}
+
+}  // namespace

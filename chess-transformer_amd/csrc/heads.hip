@@ -28,6 +28,9 @@ typedef float v16f __attribute__((ext_vector_type(16)));
 
 DEVICE v16f mfma_f32(float a, float b, v16f c) { return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0); }
 
+// nn.GELU's exact form, 0.5 v (1 + erf(v / sqrt 2)), with the device library's erf
+DEVICE float gelu(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
+
 // the 32 x 32 block sum_k A[row0 + i][k] * X[col0 + j][k] over k < D: A's rows f32 (a_bias added when BIAS), X's fp16;
 // rows past a_rows and columns past x_rows read the last one (never kept). Lane l holds, in register 4q + r,
 // the sum for A row 8q + 4(l / 32) + r and X row l % 32. D is a multiple of 64: eight steps a turn, their loads
@@ -66,7 +69,7 @@ DEVICE v16f block_products(const float* A, int a_rows, const float* a_bias, cons
 __global__ __launch_bounds__(THREADS) void move_logits_kernel(
     const half_t* __restrict__ x, const float* __restrict__ a, const float* __restrict__ a_bias, const float* __restrict__ w,
     const float* __restrict__ w_bias, const int* __restrict__ cells, const int* __restrict__ promotions, float* __restrict__ out,
-    float* __restrict__ down, int T, int D, int NN, int down_first, int moves)
+    float* __restrict__ down, int T, int D, int NN, int down_first, int moves, int out_stride, int activate)
 {
     __shared__ float logits[SQUARES * LOGIT_STRIDE];
     __shared__ float narrow[MAX_TOKENS * NARROW_STRIDE];
@@ -107,7 +110,7 @@ __global__ __launch_bounds__(THREADS) void move_logits_kernel(
 
     // the moves: cells[m] = from * 64 + to; promotions[m] = to' * 32 + column of its promotion logit, or -1 (the places
     // are masked into the tiles, so that no table entry reads outside them)
-    float* out_b = out + b * moves;
+    float* out_b = out + b * out_stride;
     for (int m = tid; m < moves; m += THREADS) {
         const int cell = cells[m], promotion = promotions[m];
         float value = logits[((cell >> 6) & 63) * LOGIT_STRIDE + (cell & 63)];
@@ -116,21 +119,128 @@ __global__ __launch_bounds__(THREADS) void move_logits_kernel(
     }
     const int width = NN - down_first;
     float* down_b = down + b * T * width;
-    for (int e = tid; e < T * width; e += THREADS) down_b[e] = narrow[(e / width) * NARROW_STRIDE + down_first + e % width];
+    for (int e = tid; e < T * width; e += THREADS) {
+        const float value = narrow[(e / width) * NARROW_STRIDE + down_first + e % width];
+        down_b[e] = activate ? gelu(value) : value;
+    }
+}
+
+// The value head of B positions (model/model.py's eval_head after board_down_project; what the reference's fused
+// heads compute in head_value_tile and head_value_kernel, model/fused_blocks.py:649-728):
+//   hidden[b][u] = gelu(sum_k c[b][k] * W1[u][k] + b1[u])          c = board_down's GELU outputs, k < K = T * 16
+//   logit[b][v]  = sum_u hidden[b][u] * W2[v][u] + b2[v]            v < bins
+//   score[b]     = sum_v exp(logit - max) * centre[v] / sum_v exp(logit - max)
+// in f32, the expected score written to the answer row's place rows[b * row_stride + score_column].
+constexpr int VALUE_TILE = 16;     // positions and hidden units a workgroup of the first layer
+constexpr int VALUE_CHUNK = 16;    // a token's board_down values: the K step of a wavefront
+constexpr int MAX_BINS = 128;
+
+// hidden = gelu(c @ W1^T + b1), 16 positions x 16 units a workgroup, on v_mfma_f32_16x16x4f32 (exact products, f32
+// sums). Lane l supplies row l % 16 of each operand and 4 consecutive k of that row (one 16-byte load), value m to
+// MFMA m, so that in MFMA m the k-group l / 16 of both operands stands for k0 + 4 (l / 16) + m. The four wavefronts
+// take the K chunks in turn (wavefront w the chunks w, w + 4, ...), and their partial tiles are added in LDS as
+// (w0 + w1) + (w2 + w3): a fixed order, so that no position's units depend on the batch it is in. Lane l ends with
+// positions 4 (l / 16) + r (register r) of unit l % 16.
+__global__ __launch_bounds__(THREADS) void value_hidden_kernel(const float* __restrict__ c, const float* __restrict__ weight,
+                                                               const float* __restrict__ bias, float* __restrict__ hidden, int B, int K, int H)
+{
+    __shared__ float partial[4][VALUE_TILE * VALUE_TILE];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p0 = blockIdx.x * VALUE_TILE, u0 = blockIdx.y * VALUE_TILE;
+    const int row = lane & 15, group = lane >> 4;
+    const float* a_row = c + (size_t)min(p0 + row, B - 1) * K + 4 * group;
+    const float* b_row = weight + (size_t)(u0 + row) * K + 4 * group;
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int chunk = wave; chunk < K / VALUE_CHUNK; chunk += 4) {
+        const float4 a4 = *reinterpret_cast<const float4*>(a_row + chunk * VALUE_CHUNK);
+        const float4 b4 = *reinterpret_cast<const float4*>(b_row + chunk * VALUE_CHUNK);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.x, b4.x, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.y, b4.y, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.z, b4.z, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a4.w, b4.w, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) partial[wave][(4 * group + r) * VALUE_TILE + row] = acc[r];
+    __syncthreads();
+    const int position = tid / VALUE_TILE, unit = tid % VALUE_TILE;
+    const float sum = (partial[0][tid] + partial[1][tid]) + (partial[2][tid] + partial[3][tid]);
+    if (p0 + position < B) hidden[(size_t)(p0 + position) * H + u0 + unit] = gelu(sum + bias[u0 + unit]);
+}
+
+// The second layer, the softmax and the expected score, a wavefront a position: lane l takes bins l and l + 64 (their
+// W2 rows read 16 bytes at a time, the position's hidden row uniform across the wavefront), f32 fma along the units in
+// order; the maximum, the exponentials' sum and the centres' weighted sum are wavefront trees.
+__global__ __launch_bounds__(THREADS) void value_score_kernel(const float* __restrict__ hidden, const float* __restrict__ weight,
+                                                              const float* __restrict__ bias, const float* __restrict__ centres,
+                                                              float* __restrict__ logits, float* __restrict__ rows, int B, int H, int bins,
+                                                              int row_stride, int score_column)
+{
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int b = blockIdx.x * 4 + wave;
+    if (b >= B) return;   // the whole wavefront: this kernel has no barriers
+    const float* h = hidden + (size_t)b * H;
+    const int v0 = lane, v1 = lane + 64;
+    const float* w0 = weight + (size_t)min(v0, bins - 1) * H;
+    const float* w1 = weight + (size_t)min(v1, bins - 1) * H;
+    float s0 = 0.0f, s1 = 0.0f;
+    for (int k = 0; k < H; k += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(h + k);
+        const float4 a = *reinterpret_cast<const float4*>(w0 + k);
+        const float4 d = *reinterpret_cast<const float4*>(w1 + k);
+        s0 = __builtin_fmaf(x.x, a.x, s0); s0 = __builtin_fmaf(x.y, a.y, s0); s0 = __builtin_fmaf(x.z, a.z, s0); s0 = __builtin_fmaf(x.w, a.w, s0);
+        s1 = __builtin_fmaf(x.x, d.x, s1); s1 = __builtin_fmaf(x.y, d.y, s1); s1 = __builtin_fmaf(x.z, d.z, s1); s1 = __builtin_fmaf(x.w, d.w, s1);
+    }
+    const bool in0 = v0 < bins, in1 = v1 < bins;
+    const float l0 = in0 ? s0 + bias[v0] : -__builtin_inff(), l1 = in1 ? s1 + bias[v1] : -__builtin_inff();
+    const float top = wave_max(fmaxf(l0, l1));
+    const float e0 = in0 ? expf(l0 - top) : 0.0f, e1 = in1 ? expf(l1 - top) : 0.0f;
+    const float total = wave_sum(e0 + e1);
+    const float weighted = wave_sum((in0 ? e0 * centres[v0] : 0.0f) + (in1 ? e1 * centres[v1] : 0.0f));
+    if (logits) {
+        if (in0) logits[(size_t)b * bins + v0] = l0;
+        if (in1) logits[(size_t)b * bins + v1] = l1;
+    }
+    if (lane == 0) rows[(size_t)b * row_stride + score_column] = weighted / total;
+}
+
+int value_head(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias, const void* centres,
+               void* value_logits, void* rows, float* hidden, int B, int K, int H, int bins, int row_stride, int score_column, hipStream_t stream)
+{
+    hipLaunchKernelGGL(value_hidden_kernel, dim3((B + VALUE_TILE - 1) / VALUE_TILE, H / VALUE_TILE), dim3(THREADS), 0, stream,
+                       (const float*)c, (const float*)hidden_weight, (const float*)hidden_bias, hidden, B, K, H);
+    if (int status = launch_status()) return status;
+    hipLaunchKernelGGL(value_score_kernel, dim3((B + 3) / 4), dim3(THREADS), 0, stream, (const float*)hidden, (const float*)out_weight,
+                       (const float*)out_bias, (const float*)centres, (float*)value_logits, (float*)rows, B, H, bins, row_stride, score_column);
+    return launch_status();
+}
+
+int check_value_head(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias,
+                     const void* centres, const void* rows, int B, int K, int H, int bins, int row_stride, int score_column)
+{
+    if (B < 0 || K <= 0 || K % VALUE_CHUNK != 0 || H <= 0 || H % VALUE_TILE != 0 || bins < 1 || bins > MAX_BINS)
+        return chess_fail(CHESS_UNSUPPORTED, "value_head takes inputs and units a multiple of %d and at most %d bins, not %d, %d and %d",
+                          VALUE_TILE, MAX_BINS, K, H, bins);
+    if (row_stride <= 0 || score_column < 0 || score_column >= row_stride)
+        return chess_fail(CHESS_INVALID_SHAPE, "value_head: the score's column %d outside rows of %d", score_column, row_stride);
+    if (!c || !hidden_weight || !hidden_bias || !out_weight || !out_bias || !centres || !rows)
+        return chess_fail(CHESS_INVALID_SHAPE, "value_head: a required pointer is null");
+    if (!aligned16(c) || !aligned16(hidden_weight) || !aligned16(out_weight))
+        return chess_fail(CHESS_MISALIGNED, "value_head reads its inputs and both weights 16 bytes a lane");
+    return CHESS_OK;
 }
 
 }  // namespace
 
 extern "C" int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
                                  const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves,
-                                 void* stream)
+                                 int out_stride, int activate, void* stream)
 {
     if (B < 0 || T < SQUARES || T > MAX_TOKENS || D <= 0 || D % 64 != 0)
         return chess_fail(CHESS_UNSUPPORTED, "move_logits takes %d to %d tokens of a width that is a multiple of 64, not %d x %d", SQUARES, MAX_TOKENS,
                           T, D);
-    if (NN <= 0 || NN > MAX_NARROW || down_first < 1 || down_first > NN || moves <= 0)
-        return chess_fail(CHESS_INVALID_SHAPE, "move_logits: %d narrow columns (at most %d), board_down from %d, %d moves", NN, MAX_NARROW,
-                          down_first, moves);
+    if (NN <= 0 || NN > MAX_NARROW || down_first < 1 || down_first > NN || moves <= 0 || out_stride < moves)
+        return chess_fail(CHESS_INVALID_SHAPE, "move_logits: %d narrow columns (at most %d), board_down from %d, %d moves in rows of %d", NN,
+                          MAX_NARROW, down_first, moves, out_stride);
     if (!x || !a || !a_bias || !w || !w_bias || !cells || !promotions || !out || !down)
         return chess_fail(CHESS_INVALID_SHAPE, "move_logits: a required pointer is null");
     if (!aligned16(x) || !aligned16(a) || !aligned16(a_bias) || !aligned16(w))
@@ -138,6 +248,21 @@ extern "C" int chess_move_logits(const void* x, const void* a, const void* a_bia
     if (B == 0) return CHESS_OK;
     hipLaunchKernelGGL(move_logits_kernel, dim3(B), dim3(THREADS), 0, (hipStream_t)stream, (const half_t*)x, (const float*)a,
                        (const float*)a_bias, (const float*)w, (const float*)w_bias, (const int*)cells, (const int*)promotions, (float*)out,
-                       (float*)down, T, D, NN, down_first, moves);
+                       (float*)down, T, D, NN, down_first, moves, out_stride, activate);
     return launch_status();
+}
+
+extern "C" int chess_value_head(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias,
+                                const void* centres, void* value_logits, void* rows, void* workspace, long long workspace_bytes, int B, int K, int H,
+                                int bins, int row_stride, int score_column, void* stream)
+{
+    if (int status = check_value_head(c, hidden_weight, hidden_bias, out_weight, out_bias, centres, rows, B, K, H, bins, row_stride, score_column))
+        return status;
+    if (!workspace || workspace_bytes < (long long)B * H * (long long)sizeof(float))
+        return chess_fail(CHESS_INVALID_SHAPE, "value_head's workspace holds the hidden layer, %lld bytes, not %lld", (long long)B * H * 4LL,
+                          workspace_bytes);
+    if (!aligned16(workspace)) return chess_fail(CHESS_MISALIGNED, "value_head reads its workspace 16 bytes a lane");
+    if (B == 0) return CHESS_OK;
+    return value_head(c, hidden_weight, hidden_bias, out_weight, out_bias, centres, value_logits, rows, (float*)workspace, B, K, H, bins, row_stride,
+                      score_column, (hipStream_t)stream);
 }

@@ -70,35 +70,30 @@ LEAN_ROW = TOKENS_PER_BOARD + 2 * LEAN_COLUMNS
 
 
 @torch.library.custom_op("chess::lean_answers", mutates_args=())
-def lean_answers(logits: torch.Tensor, score: torch.Tensor, rows: torch.Tensor, columns_at: int, columns: int) -> torch.Tensor:
-    """answers[b][j] = the answer row (logits[b] then score[b]) at the int16 index stored at byte columns_at + 2j of
-    rows[b]: reference Lane.answer's torch.cat and torch.gather (engine/inference.py:134-137) as one launch."""
-    if logits.dtype != torch.float32 or score.dtype != torch.float32 or rows.dtype != torch.uint8:
-        raise ValueError(f"lean_answers takes f32 logits and scores and uint8 rows, not {logits.dtype}, {score.dtype}, {rows.dtype}")
-    if logits.dim() != 2 or score.shape != logits.shape[:1] or rows.dim() != 2 or rows.shape[0] != logits.shape[0]:
-        raise ValueError(f"lean_answers: logits {tuple(logits.shape)}, score {tuple(score.shape)}, rows {tuple(rows.shape)}")
-    library = library_for(logits.device)
-    logits, score, rows = logits.contiguous(), score.contiguous(), rows.contiguous()
-    answers = torch.empty(logits.shape[0], columns, device=logits.device, dtype=torch.float32)
-    code = library.chess_lean_answers(pointer(logits), pointer(score), pointer(rows), pointer(answers), logits.shape[0], logits.shape[1],
-                                      rows.shape[1], columns_at, columns, stream_of(logits.device))
+def lean_answers(answers: torch.Tensor, rows: torch.Tensor, columns_at: int, columns: int) -> torch.Tensor:
+    """out[b][j] = answers[b] (a board's answer row: the move logits, then the expected score) at the int16 index stored at
+    byte columns_at + 2j of rows[b]: reference Lane.answer's torch.gather (engine/inference.py:134-137) as one launch."""
+    if answers.dtype != torch.float32 or rows.dtype != torch.uint8:
+        raise ValueError(f"lean_answers takes f32 answer rows and uint8 board rows, not {answers.dtype} and {rows.dtype}")
+    if answers.dim() != 2 or rows.dim() != 2 or rows.shape[0] != answers.shape[0]:
+        raise ValueError(f"lean_answers: answer rows {tuple(answers.shape)}, board rows {tuple(rows.shape)}")
+    library = library_for(answers.device)
+    answers, rows = answers.contiguous(), rows.contiguous()
+    out = torch.empty(answers.shape[0], columns, device=answers.device, dtype=torch.float32)
+    code = library.chess_lean_answers(pointer(answers), pointer(rows), pointer(out), answers.shape[0], answers.shape[1], rows.shape[1], columns_at,
+                                      columns, stream_of(answers.device))
     check(code, "lean_answers")
-    return answers
+    return out
 
 
 @lean_answers.register_fake
-def _(logits, score, rows, columns_at, columns):
-    return logits.new_empty(logits.shape[0], columns)
+def _(answers, rows, columns_at, columns):
+    return answers.new_empty(answers.shape[0], columns)
 
 
 #a lean lane's answers for boards whose rows (tokens, then LEAN_COLUMNS int16 indices) are rows
 def lean_rows(outputs: tuple[torch.Tensor, torch.Tensor] | torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
-    if isinstance(outputs, torch.Tensor):
-        logits, score = outputs[:, :-1], outputs[:, -1]
-    else:
-        move_logits, value_logits = outputs
-        logits, score = move_logits.float(), expected_score(value_logits)
-    return lean_answers(logits, score, rows, TOKENS_PER_BOARD, LEAN_COLUMNS)
+    return lean_answers(answer_rows(outputs), rows, TOKENS_PER_BOARD, LEAN_COLUMNS)
 
 
 #the L2 a position's activations take between a block's kernels, per unit of the model's width (reference :25-32)

@@ -3,8 +3,8 @@ that the int8 path uses -- the operators chess::template_attention and chess::li
 link_input_mixes, tile_for -- and FusedTransformer, the network the engine calls.
 
 The operators launch the HIP kernels of libchess_hip.so, the input embedding included (chess::board_embedding, which finds
-the square features from the boards as the reference's board_embedding_kernel does). The heads run as torch operations on
-the GPU, the reference's own path on GPUs without its fused heads (reference fused_blocks.py:863-874).
+the square features from the boards as the reference's board_embedding_kernel does) and the heads (chess::heads: the move
+logits written into the answer rows, the eval head and the expected score), as on the reference's GPUs with fused ends.
 """
 from __future__ import annotations
 
@@ -18,7 +18,7 @@ from torch import nn
 from model import hip_kernels
 from model.encoding import NUM_SQUARES, TOKENS_PER_BOARD
 from model.hip_kernels import aligned, check, library_for, pointer, stream_of
-from model.model import EDGE, KING, KNIGHT, NO_PIECE, PAWN, QUEEN, THEIRS, ChessTransformer, TransformerBlock
+from model.model import EDGE, KING, KNIGHT, NO_PIECE, PAWN, QUEEN, THEIRS, ChessTransformer, TransformerBlock, value_bin_centres
 
 LINEAR_DEPTH, GROUP_M = 32, 8
 FEATURE_SLOTS = 23
@@ -346,30 +346,40 @@ class InputEmbedding(nn.Module):
         return board_embedding(board_state, self.rays, self.jumps, self.offsets, self.embed.weight, self.position_embed, self.features.table)
 
 
-#logits[i, j] = (W_f x_i + b_f) . (W_t x_j + b_t) / sqrt(d) = a_i . x_j + s_i: from and to as one d x d matmul (a)
-#the policy head's move logits after its `a` matmul and board_down's inputs (reference fused_blocks.py:866-871), one launch
-@torch.library.custom_op("chess::move_logits", mutates_args=())
-def move_logits(x: torch.Tensor, a: torch.Tensor, a_bias: torch.Tensor, narrow_weight: torch.Tensor, narrow_bias: torch.Tensor, cells: torch.Tensor,
-                promotions: torch.Tensor, down_first: int) -> tuple[torch.Tensor, torch.Tensor]:
+def _check_head_operands(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, what: str) -> None:
     B, T, D = x.shape
     for tensor, dtype, name in ((x, torch.float16, "x"), (a, torch.float32, "a"), (a_bias, torch.float32, "a_bias"),
                                 (narrow_weight, torch.float32, "narrow_weight"), (narrow_bias, torch.float32, "narrow_bias"),
                                 (cells, torch.int32, "cells"), (promotions, torch.int32, "promotions")):
         if tensor.dtype != dtype:
-            raise ValueError(f"move_logits' {name} is {tensor.dtype}, the kernel takes {dtype}")
+            raise ValueError(f"{what}'s {name} is {tensor.dtype}, the kernel takes {dtype}")
     if a.shape != x.shape or a_bias.numel() != D or narrow_weight.shape[1] != D or narrow_bias.numel() != narrow_weight.shape[0]:
-        raise ValueError(f"move_logits: x {tuple(x.shape)}, a {tuple(a.shape)}, a_bias {a_bias.numel()}, narrow {tuple(narrow_weight.shape)}")
+        raise ValueError(f"{what}: x {tuple(x.shape)}, a {tuple(a.shape)}, a_bias {a_bias.numel()}, narrow {tuple(narrow_weight.shape)}")
     if cells.shape != promotions.shape:
-        raise ValueError("move_logits: a cell and a promotion place for every move")
+        raise ValueError(f"{what}: a cell and a promotion place for every move")
+
+
+def _launch_move_logits(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first, out, out_stride, activate) -> torch.Tensor:
+    B, T, D = x.shape
     library = library_for(x.device)
     x, a, a_bias, narrow_weight = aligned(x), aligned(a), aligned(a_bias), aligned(narrow_weight)
     narrow = narrow_weight.shape[0]
-    out = torch.empty(B, cells.numel(), device=x.device, dtype=torch.float32)
     down = torch.empty(B, T, narrow - down_first, device=x.device, dtype=torch.float32)
     code = library.chess_move_logits(pointer(x), pointer(a), pointer(a_bias), pointer(narrow_weight), pointer(narrow_bias.contiguous()),
                                      pointer(cells.contiguous()), pointer(promotions.contiguous()), pointer(out), pointer(down), B, T, D, narrow,
-                                     down_first, cells.numel(), stream_of(x.device))
+                                     down_first, cells.numel(), out_stride, int(activate), stream_of(x.device))
     check(code, "move_logits")
+    return down
+
+
+#logits[i, j] = (W_f x_i + b_f) . (W_t x_j + b_t) / sqrt(d) = a_i . x_j + s_i: from and to as one d x d matmul (a)
+#the policy head's move logits after its `a` matmul and board_down's inputs (reference fused_blocks.py:866-871), one launch
+@torch.library.custom_op("chess::move_logits", mutates_args=())
+def move_logits(x: torch.Tensor, a: torch.Tensor, a_bias: torch.Tensor, narrow_weight: torch.Tensor, narrow_bias: torch.Tensor, cells: torch.Tensor,
+                promotions: torch.Tensor, down_first: int) -> tuple[torch.Tensor, torch.Tensor]:
+    _check_head_operands(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, "move_logits")
+    out = torch.empty(x.shape[0], cells.numel(), device=x.device, dtype=torch.float32)
+    down = _launch_move_logits(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first, out, cells.numel(), False)
     return out, down
 
 
@@ -377,6 +387,43 @@ def move_logits(x: torch.Tensor, a: torch.Tensor, a_bias: torch.Tensor, narrow_w
 def _(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first):
     B, T, _ = x.shape
     return x.new_empty(B, cells.numel(), dtype=torch.float32), x.new_empty(B, T, narrow_weight.shape[0] - down_first, dtype=torch.float32)
+
+
+#the heads from the `a` matmul on: the answer rows (the move logits, then the expected score; reference engine/inference.py:19-23,
+#fused_blocks.py:697-728) and the value logits, in three launches: the move logits into the rows with board_down's GELU outputs,
+#then the eval head's two layers and the expected score (its hidden layer in a workspace of B x H f32)
+@torch.library.custom_op("chess::heads", mutates_args=())
+def heads(x: torch.Tensor, a: torch.Tensor, a_bias: torch.Tensor, narrow_weight: torch.Tensor, narrow_bias: torch.Tensor, cells: torch.Tensor,
+          promotions: torch.Tensor, down_first: int, hidden_weight: torch.Tensor, hidden_bias: torch.Tensor, out_weight: torch.Tensor,
+          out_bias: torch.Tensor, centres: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    _check_head_operands(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, "heads")
+    for tensor, name in ((hidden_weight, "hidden_weight"), (hidden_bias, "hidden_bias"), (out_weight, "out_weight"), (out_bias, "out_bias"),
+                         (centres, "centres")):
+        if tensor.dtype != torch.float32:
+            raise ValueError(f"heads' {name} is {tensor.dtype}, the kernel takes f32")
+    B, T, _ = x.shape
+    moves = cells.numel()
+    H, K = hidden_weight.shape
+    bins = out_weight.shape[0]
+    if K != T * (narrow_weight.shape[0] - down_first) or out_weight.shape[1] != H or hidden_bias.numel() != H or out_bias.numel() != bins \
+            or centres.numel() != bins:
+        raise ValueError(f"heads: the eval head {tuple(hidden_weight.shape)} then {tuple(out_weight.shape)} for {T} tokens of "
+                         f"{narrow_weight.shape[0] - down_first} board_down values")
+    rows = torch.empty(B, moves + 1, device=x.device, dtype=torch.float32)
+    value_logits = torch.empty(B, bins, device=x.device, dtype=torch.float32)
+    activated = _launch_move_logits(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first, rows, moves + 1, True)
+    workspace = torch.empty(B, H, device=x.device, dtype=torch.float32)
+    code = library_for(x.device).chess_value_head(pointer(activated), pointer(aligned(hidden_weight)), pointer(hidden_bias.contiguous()),
+                                                  pointer(aligned(out_weight)), pointer(out_bias.contiguous()), pointer(centres.contiguous()),
+                                                  pointer(value_logits), pointer(rows), pointer(workspace), workspace.numel() * 4, B, K, H, bins,
+                                                  moves + 1, moves, stream_of(x.device))
+    check(code, "value_head")
+    return rows, value_logits
+
+
+@heads.register_fake
+def _(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first, hidden_weight, hidden_bias, out_weight, out_bias, centres):
+    return x.new_empty(x.shape[0], cells.numel() + 1, dtype=torch.float32), x.new_empty(x.shape[0], out_weight.shape[0], dtype=torch.float32)
 
 
 def move_places(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor]:
@@ -400,10 +447,11 @@ def head_weights(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor, t
 
 
 class FusedTransformer(nn.Module):
-    """ChessTransformer.forward with FusedBlocks, for inference (reference fused_blocks.py:829-874, its path without fused ends):
-    returns the move logits and the value logits."""
+    """ChessTransformer.forward with FusedBlocks, for inference (reference fused_blocks.py:829-874). With fused_heads (the default,
+    as on the reference's GPUs with fused ends) the forward returns the answer rows, B x (moves + 1) f32: the move logits, then
+    the expected score; else the move logits and the value logits. Both come from the same launches; answer_rows takes either."""
 
-    def __init__(self, model: ChessTransformer):
+    def __init__(self, model: ChessTransformer, fused_heads: bool = True):
         super().__init__()
         self.d_model = model.d_model
         self.input_embedding = InputEmbedding(model)
@@ -411,8 +459,7 @@ class FusedTransformer(nn.Module):
         self.encoder = nn.ModuleList(FusedBlock(block) for block in model.encoder)
         link_input_mixes(list(self.encoder))
         prepare(model.templates)
-        self.fused_heads = False
-        self.board_down_activation, self.eval_head = model.board_down_project[1], model.eval_head
+        self.fused_heads = fused_heads
         for name in ("from_squares", "to_squares", "promotion_move_ids", "promotion_to_squares", "promotion_pieces"):
             self.register_buffer(name, getattr(model, name))
         self.a_weight, self.a_bias, self.narrow_weight, self.narrow_bias = (nn.Parameter(tensor, requires_grad=False) for tensor in head_weights(model))
@@ -421,19 +468,23 @@ class FusedTransformer(nn.Module):
         cells, promotion_places = move_places(model)
         self.register_buffer("move_cells", cells)
         self.register_buffer("move_promotions", promotion_places)
+        hidden, out = model.eval_head[0], model.eval_head[2]
+        value = {"hidden_weight": hidden.weight, "hidden_bias": hidden.bias, "out_weight": out.weight, "out_bias": out.bias,
+                 "centres": value_bin_centres(out.out_features, out.weight.device)}
+        for name, tensor in value.items():
+            self.register_buffer(name, tensor.detach().float().contiguous())
 
-    def forward(self, board_state: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    def forward(self, board_state: torch.Tensor) -> torch.Tensor | tuple[torch.Tensor, torch.Tensor]:
         embed_state = self.input_embedding(board_state)
         original_board_embed = embed_state
         for block in self.encoder:
             embed_state = block(embed_state, self.templates, original_board_embed)
-        model_output = rms_norm(embed_state, self.ln.weight, norm_eps(self.ln, embed_state))
+        rows, value_logits = self.answers(rms_norm(embed_state, self.ln.weight, norm_eps(self.ln, embed_state)))
+        return rows if self.fused_heads else (rows[:, :-1], value_logits)
 
-        with torch.autocast(device_type=board_state.device.type, enabled=False):
-            #a = x @ a_weight in f32 sums; its f32 bias, the narrow products (s, the promotion logits, board_down_project's), the
-            #bilinear logits and the gathers of the moves are one launch
+    def answers(self, model_output: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """The answer rows and the value logits of the final norm's rows (fp16): `a` = x @ a_weight with f32 sums, then the heads."""
+        with torch.autocast(device_type=model_output.device.type, enabled=False):
             a = linear(model_output, self.a_weight, accumulate_fp32=True)
-            combined_logits, board_down = move_logits(model_output, a, self.a_bias, self.narrow_weight, self.narrow_bias, self.move_cells,
-                                                      self.move_promotions, self.down_columns.start)
-            compressed_board = self.board_down_activation(board_down).reshape(board_state.shape[0], -1)
-            return combined_logits, self.eval_head(compressed_board)
+            return heads(model_output, a, self.a_bias, self.narrow_weight, self.narrow_bias, self.move_cells, self.move_promotions,
+                         self.down_columns.start, self.hidden_weight, self.hidden_bias, self.out_weight, self.out_bias, self.centres)

@@ -93,19 +93,33 @@ int chess_board_embedding(const void* boards, int code_bytes, const void* rays, 
  * fused ends): x[B, T, D] the final norm's rows (fp16), a[B, T, D] = x @ a_weight (f32, rows 0..63 read), a_bias[D],
  * w[NN, D] and w_bias[NN] the narrow projections (f32: s, the promotion logits, board_down's inputs from down_first),
  * cells[moves] = from * 64 + to and promotions[moves] = to' * 32 + column of the move's promotion logit or -1 (int32).
- * out[B, moves] f32 = ((a[from] + a_bias) . x[to]) + narrow[from][0] (+ narrow[to'][column]); down[B, T, NN - down_first]
- * f32 = narrow[t][down_first..NN). 64 <= T <= 96, D % 64 == 0, NN <= 32. Replaces the torch ops of :866-871 (the f32
- * linear, the transposed bmm, the gathers and the promotion sum). */
+ * out[b * out_stride + m] f32 = ((a[from] + a_bias) . x[to]) + narrow[from][0] (+ narrow[to'][column]), m < moves
+ * (out_stride = moves + 1 writes the answer rows' logits in place); down[B, T, NN - down_first] f32 =
+ * narrow[t][down_first..NN), through nn.GELU when activate (board_down_project's activation, the value head's input).
+ * 64 <= T <= 96, D % 64 == 0, NN <= 32. Replaces the torch ops of :866-871 (the f32 linear, the transposed bmm, the
+ * gathers and the promotion sum). */
 int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
-                      const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves, void* stream);
+                      const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves, int out_stride,
+                      int activate, void* stream);
 
-/* The lean lanes' answers (engine/inference.py:131-137, Lane.answer's gather on a lean lane): rows[B][row_bytes] hold
- * at byte columns_at `columns` little-endian int16 indices into a board's answer row, the moves' logits then the
- * expected score (:19-23; the row layout of engine/selfplay_rs/src/lib.rs:331-333). answers[B][columns] f32 =
- * index < moves ? logits[b][index] (logits f32 [B][moves]) : score[b] (f32 [B]); an index outside [0, moves] gives
- * NaN. Replaces the torch.cat of the answer rows and the torch.gather. rows, row_bytes and columns_at even. */
-int chess_lean_answers(const void* logits, const void* score, const void* rows, void* answers, int B, int moves, int row_bytes,
-                       int columns_at, int columns, void* stream);
+/* The value head of B positions (the eval head after board_down_project, model/model.py:200-201, and the expected score,
+ * :37-41; the reference's fused head_value_tile / head_value_kernel, model/fused_blocks.py:649-728): from c[B, K] f32,
+ * board_down's activated outputs (K = T * 16), hidden[b][u] = gelu(c[b] . hidden_weight[u] + hidden_bias[u]) (u < H,
+ * hidden_weight [H, K] f32), logit[b][v] = hidden[b] . out_weight[v] + out_bias[v] (v < bins <= 128, out_weight
+ * [bins, H] f32), and rows[b * row_stride + score_column] = sum_v softmax(logit[b])[v] * centres[v]; value_logits[B, bins]
+ * f32 as well unless NULL. All f32, nn.GELU's erf form. The hidden layer goes through workspace (at least B * H * 4
+ * bytes, 16-byte aligned), which the call allocates nothing for. K % 16 == 0, H % 16 == 0. */
+int chess_value_head(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias,
+                     const void* centres, void* value_logits, void* rows, void* workspace, long long workspace_bytes, int B, int K, int H,
+                     int bins, int row_stride, int score_column, void* stream);
+
+/* The lean lanes' answers (engine/inference.py:131-137, Lane.answer's gather on a lean lane): rows[B][row_bytes] hold at
+ * byte columns_at `columns` little-endian int16 indices into a board's answer row (answer_rows[B][width] f32: the moves'
+ * logits then the expected score, :19-23; the row layout of engine/selfplay_rs/src/lib.rs:331-333). answers[B][columns]
+ * f32 = answer_rows[b][index]; an index outside [0, width) gives NaN. Replaces the torch.gather from the answer rows.
+ * rows, row_bytes and columns_at even. */
+int chess_lean_answers(const void* answer_rows, const void* rows, void* answers, int B, int width, int row_bytes, int columns_at, int columns,
+                       void* stream);
 
 /* Fills table[0..6] with hipSetDevice, hipMemcpyAsync, hipGraphLaunch, hipEventRecord, hipEventSynchronize,
  * hipStreamSynchronize, hipGetErrorString: the address table of engine/cuda_runtime.py:17-49 (CudaRuntime.CALLS

@@ -86,8 +86,10 @@ def compare_with_oracle(model: ChessTransformer, settings: dict, boards: torch.T
     weights = weights or nearest_int8_weights(model)
     state = {name: value.clone() for name, value in model.state_dict().items()}
     network = int8_network(copy.deepcopy(model).to(device), weights)
+    network.fused_heads = False
     with torch.no_grad():
         logits, values = network(boards.to(device))
+    network.fused_heads = True
     expected_logits, expected_values = oracle_network.int8_forward(state, settings, weights, boards)
     logits, values = logits.float().cpu(), values.float().cpu()
     assert (logits - expected_logits).abs().max() < 2e-2
@@ -141,6 +143,32 @@ def test_the_move_logits_are_the_heads_torch_ops(device, settings):
     assert logits.shape == (B, len(fused.from_squares)) and down.shape == (B, T, narrow.shape[-1] - fused.down_columns.start)
     assert torch.allclose(logits.double(), expected, atol=1e-4, rtol=1e-4)
     assert torch.allclose(down.double(), narrow[..., fused.down_columns], atol=1e-4, rtol=1e-4)
+
+
+@pytest.mark.parametrize("settings", [SMALL, FULL])
+def test_the_heads_are_the_oracles(device, settings):
+    """chess::heads from the final norm's rows: the value logits and the expected score against the oracle's heads in float64
+    (the reference's model/model.py:264-268 and expected_score), the move logits against the torch ops of the heads' own
+    formulation (the fp16 `a` of reference fused_blocks.py:815-823), and the answer rows as the forward returns them."""
+    model = make_model(settings, seed=13)
+    state = {name: value.clone() for name, value in model.state_dict().items()}
+    fused = fused_blocks.FusedTransformer(copy.deepcopy(model).scale_residual_stream(FP16_RESIDUAL_SCALE).half_except_heads(torch.float16)).to(device)
+    torch.manual_seed(13)
+    B, D = 37, settings["d_model"]
+    x = torch.randn(B, 70, D).half()
+    with torch.no_grad():
+        rows, value_logits = fused.answers(x.to(device))
+    moves, values = oracle_network._heads(state, x.double(), settings)
+    rows, value_logits = rows.cpu().double(), value_logits.cpu().double()
+    assert rows.shape == (B, moves.shape[1] + 1) and value_logits.shape == values.shape
+    assert torch.allclose(value_logits, values, atol=1e-4, rtol=1e-4)
+    assert torch.allclose(rows[:, -1], expected_score(values.double()).double(), atol=1e-4)
+    a = x.double() @ fused.a_weight.cpu().double() + fused.a_bias.cpu().double()
+    narrow = x.double() @ fused.narrow_weight.cpu().double().T + fused.narrow_bias.cpu().double()
+    logits = (a[:, :64] @ x[:, :64].double().transpose(1, 2) + narrow[:, :64, :1])[:, fused.from_squares.cpu(), fused.to_squares.cpu()]
+    logits[:, fused.promotion_move_ids.cpu()] += narrow[:, :64][..., fused.promotion_columns][:, fused.promotion_to_squares.cpu(),
+                                                                                               fused.promotion_pieces.cpu()]
+    assert torch.allclose(rows[:, :-1], logits, atol=1e-4, rtol=1e-4)
 
 
 def test_tiles_change_no_answer(device, monkeypatch):
