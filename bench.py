@@ -47,11 +47,15 @@ def log(message: str) -> None:
 
 def synthetic_model(settings: dict, seed: int = 0):
     """Random-init weights as BASELINE states them: linear weights and biases N(0, 0.02), norm gains 1 + N(0, 0.1), templates
-    N(0, 0.5), square-feature table N(0, 0.1), the input mixed in (residual 0.8, input 0.5)."""
+    N(0, 0.5), square-feature table N(0, 0.1), the input mixed in (residual 0.8, input 0.5). Drawn with numpy's generator
+    (PCG64, float32 normals), whose stream is the same on every machine, so that the GPU box builds the very network the
+    committed expected outputs (tests/golden/) were computed for."""
+    import numpy as np
     import torch
     from model.model import ChessTransformer
-    torch.manual_seed(seed)
+    rng = np.random.default_rng(seed)
     model = ChessTransformer(**settings).eval()
+    normal = lambda parameter, std: torch.from_numpy(rng.standard_normal(tuple(parameter.shape), dtype=np.float32) * np.float32(std))
     with torch.no_grad():
         for name, parameter in model.named_parameters():
             if name.endswith("residual_scale"):
@@ -59,22 +63,26 @@ def synthetic_model(settings: dict, seed: int = 0):
             elif name.endswith("input_scale"):
                 parameter.fill_(0.5)
             elif name == "templates":
-                parameter.normal_(std=0.5)
+                parameter.copy_(normal(parameter, 0.5))
             elif name == "square_features.table":
-                parameter.normal_(std=0.1)
+                parameter.copy_(normal(parameter, 0.1))
             elif "norm" in name or name.startswith("ln") or ".ln" in name:
-                parameter.copy_(1 + 0.1 * torch.randn_like(parameter))
+                parameter.copy_(1 + normal(parameter, 0.1))
             else:
-                parameter.normal_(std=0.02)
+                parameter.copy_(normal(parameter, 0.02))
     return model
 
 
-def random_boards(count: int, seed: int = 0):
+POSITIONS = ROOT / "tests" / "golden" / "positions.npz"
+
+
+def legal_boards(count: int, first: int = 0):
+    """count seeded random legal positions (0-80 random legal plies from the start; tests/golden/positions.npz, 4,096 of them)
+    from the first-th on, as int64 tokens [count, 70], wrapping round the fixture past its end."""
+    import numpy as np
     import torch
-    generator = torch.Generator().manual_seed(seed)
-    boards = torch.randint(0, 13, (count, TOKENS), generator=generator)
-    boards[:, 64:] = torch.tensor([14, 16, 16, 16, 16, 17])
-    return boards
+    tokens = np.load(POSITIONS)["tokens"]
+    return torch.from_numpy(tokens[(first + np.arange(count)) % len(tokens)].astype(np.int64))
 
 
 class Graphed:
@@ -83,7 +91,7 @@ class Graphed:
     def __init__(self, network, batch: int, device):
         import torch
         self.stream = torch.cuda.Stream(device)
-        self.boards = random_boards(batch, seed=batch).to(device)
+        self.boards = legal_boards(batch).to(device)
         self.stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(self.stream), torch.no_grad():
             for _ in range(2):
@@ -225,7 +233,7 @@ def in_network_launches(network, batch: int, device, passes: int = 4) -> list[fl
         pairs.append((begin, end))
         return out
 
-    boards = random_boards(batch, seed=batch).to(device)
+    boards = legal_boards(batch).to(device)
     with torch.no_grad():
         network(boards)
         torch.cuda.synchronize(device)
@@ -316,19 +324,60 @@ def pmc_summary(folder: Path, batch: int) -> int:
     return 0
 
 
-def cpu_baseline(model_state: dict, sample: int) -> dict:
-    """The CPU oracle's fp32 forward (the reference's CPU path, model/model.py:245-270) on a bounded sample, this host's cores."""
+CONFIG0 = {"d_model": 256, "num_layers": 4, "n_heads": 8, "kv_heads": 8, "mlp_hidden": 1024, "value_bins": 128, "position_templates": 8}
+
+
+def usable_cpus() -> int:
+    """The CPUs this process may run on: its affinity set, within the container's CPU quota (cgroup v2 cpu.max) if it has one."""
+    count = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    try:
+        quota, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if quota != "max":
+            count = min(count, max(1, int(quota) // int(period)))
+    except (OSError, ValueError):
+        pass
+    return count
+
+
+def time_cpu_forward(state: dict, settings: dict, batch: int, threads: int, runs: int, warmups: int) -> dict:
+    """p50 / p99 ms of the CPU forward of batch legal positions (oracle/network.py fp32_forward: the reference's CPU path,
+    model/model.py:245-270, as engine/inference.py:274-278 serves it) on threads torch threads, over runs after warmups."""
     import torch
     from oracle import network as oracle_network
-    threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
-    boards = random_boards(sample, seed=11)
-    oracle_network.fp32_forward(model_state, SETTINGS, boards[:2])
-    start = time.perf_counter()
-    oracle_network.fp32_forward(model_state, SETTINGS, boards)
-    seconds = time.perf_counter() - start
-    return {"value": round(sample / seconds, 2), "unit": "positions/s", "cores": threads, "kind": "port",
-            "sample": f"{sample} positions, one fp32 forward of the d512 x 28 network (oracle/network.py fp32_forward, torch CPU), {seconds:.1f} s"}
+    boards = legal_boards(batch, 1024)
+    for _ in range(warmups):
+        oracle_network.fp32_forward(state, settings, boards)
+    times = []
+    for _ in range(runs):
+        start = time.perf_counter()
+        oracle_network.fp32_forward(state, settings, boards)
+        times.append((time.perf_counter() - start) * 1e3)
+    times.sort()
+    p50, p99 = times[len(times) // 2], times[min(len(times) - 1, math.ceil(0.99 * len(times)) - 1)]
+    return {"batch": batch, "threads": threads, "runs": runs, "warmups": warmups, "p50_ms": round(p50, 2), "p99_ms": round(p99, 2),
+            "positions_per_s": round(batch / p50 * 1e3, 2)}
+
+
+def cpu_baseline(model_state: dict, runs: int = 20, warmups: int = 3) -> dict:
+    """The CPU baseline of BASELINE.md's protocol: the fp32 CPU forward of config 0 (d256 x 4, batch 64) and config 3 (the d512 x
+    28 network, batch 64), p50 and p99 over runs after warmups, on every CPU this process may use and on one thread (the
+    engine's own setting, reference engine/uci.py:557). The one-thread d512 x 28 figure takes batches of 8 (a forward of 64
+    takes about 15 s on one core), still 20 runs. value: config 3 on all usable threads, positions/s at the p50."""
+    import torch
+    threads = usable_cpus()
+    config0 = synthetic_model(CONFIG0, 1)
+    config0_state = {name: value.clone() for name, value in config0.state_dict().items()}
+    results = {"config0_all_threads": time_cpu_forward(config0_state, CONFIG0, 64, threads, runs, warmups),
+               "config0_one_thread": time_cpu_forward(config0_state, CONFIG0, 64, 1, runs, warmups),
+               "config3_all_threads": time_cpu_forward(model_state, SETTINGS, 64, threads, runs, warmups),
+               "config3_one_thread": time_cpu_forward(model_state, SETTINGS, 8, 1, runs, warmups)}
+    torch.set_num_threads(threads)
+    headline = results["config3_all_threads"]
+    return {"value": headline["positions_per_s"], "unit": "positions/s", "cores": threads, "kind": "port",
+            "sample": f"config 3: the d512 x 28 network's fp32 CPU forward (oracle/network.py fp32_forward, torch CPU) of 64 seeded legal "
+                      f"positions, p50 of {runs} runs after {warmups} warm-ups, {threads} threads",
+            "host_cpus": os.cpu_count(), "usable_cpus": threads, **results}
 
 
 def main() -> int:
@@ -340,7 +389,7 @@ def main() -> int:
     parser.add_argument("--latency-batch", type=int, default=64)
     parser.add_argument("--sweep", action="store_true", help="also time batches 1, 16, 64, 256, 1024, 4096")
     parser.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    parser.add_argument("--cpu-sample", type=int, default=256)
+    parser.add_argument("--cpu-runs", type=int, default=20, help="timed CPU forwards per configuration (after 3 warm-ups)")
     parser.add_argument("--no-standalone", action="store_true", help="skip the standalone GEMM and attention configs")
     parser.add_argument("--kernel-only", action="store_true", help="run only the dominant kernel and a copy, for counter runs")
     parser.add_argument("--pmc-summary", type=Path, help="summarise the FETCH_SIZE / WRITE_SIZE runs under this folder")
@@ -409,9 +458,11 @@ def main() -> int:
 
     baseline = None
     if not arguments.no_cpu:
-        log(f"CPU baseline: fp32 forward of {arguments.cpu_sample} positions")
-        baseline = cpu_baseline(state, arguments.cpu_sample)
-        log(f"  {baseline['value']} positions/s on {baseline['cores']} threads")
+        log(f"CPU baseline: fp32 forwards of configs 0 and 3, {arguments.cpu_runs} runs each on {usable_cpus()} threads and on one")
+        baseline = cpu_baseline(state, arguments.cpu_runs)
+        for name in ("config0_all_threads", "config0_one_thread", "config3_all_threads", "config3_one_thread"):
+            run = baseline[name]
+            log(f"  {name}: batch {run['batch']} on {run['threads']} threads, p50 {run['p50_ms']} ms, {run['positions_per_s']} positions/s")
 
     result = {"metric": "positions/sec at batch 1024 (28L int8 net)", "value": round(positions_per_s, 1), "unit": "positions/s", "n_gpus": 1,
               "steps": arguments.steps, "warmup": arguments.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,

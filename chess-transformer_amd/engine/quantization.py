@@ -1,15 +1,16 @@
-"""The int8 weights of a checkpoint: the module API of the reference's engine/quantization.py.
+"""The int8 weights of a checkpoint: the module API of the reference's engine/quantization.py (int8_weights,
+compute_int8_weights, gptq, block_errors, cached_weights_path, cache_folder and the settings that name the cache).
 
-Produces {layer: {"projection" | "gate_up" | "down": (int8 N x K, f32 scale[N])}} for every block but the
-last FP16_LAST_LAYERS, laid out as Int8Block reads them (reference quantization.py:122-140): projection
-is Q | K | V | template_mix, gate_up the gate's rows then up's, down zero-padded to down_inputs(hidden)
-and rotated by the block-diagonal Hadamard matrix / 32, so that (x H)(W H / 32)^T = x W^T. Rounding is
-GPTQ (Frantar et al. 2022) in float64 on the input Hessians of calibration positions. The cache of
-computed weights and its file names are the reference's (quantization.py:174-223), so a cached file
-is found by either.
+The result is {layer: {"projection" | "gate_up" | "down": (int8 [N, K], f32 scale [N])}} for every block but the last
+FP16_LAST_LAYERS, in the layout Int8Block reads (reference quantization.py:122-140): projection is Q | K | V |
+template_mix, gate_up the gate's rows then up's, and down zero-padded to down_inputs(hidden) and rotated by the
+block-diagonal Sylvester matrix / 32, so that (x H)(W H / 32)^T = x W^T. Rounding is GPTQ (Frantar et al., 2022) in
+float64 on the Hessians of each matmul's inputs over calibration positions; with a diagonal Hessian it is round to
+nearest (nearest, nearest_int8_weights), which the random-init networks of the tests and the benchmark take.
 
-The calibration positions come from engine/Carlsen.pgn through python-chess, as in the reference;
-where python-chess is not installed, callers pass encoded boards themselves.
+The cache's file name is kept as the reference forms it -- the checkpoint's sha256 and a 16-hex-digit hash of the rounding
+settings -- so that a cached file is found by either. The calibration positions are read with python-chess, which only
+that step needs; without it, callers pass encoded boards (and their legal moves) themselves.
 """
 from __future__ import annotations
 
@@ -17,7 +18,6 @@ import argparse
 import hashlib
 import os
 import sys
-from contextlib import suppress
 from pathlib import Path
 
 import torch
@@ -35,17 +35,20 @@ CACHE_VARIABLE = "CHESS_TRANSFORMER_INT8_CACHE"
 
 
 def cache_folder() -> Path | None:
-    """The environment's named folder, else ~/.cache/chess_transformer/int8; None without a home folder."""
-    if os.environ.get(CACHE_VARIABLE):
-        return Path(os.environ[CACHE_VARIABLE])
+    """The folder the environment names, else ~/.cache/chess_transformer/int8; None when there is no home folder."""
+    named = os.environ.get(CACHE_VARIABLE)
+    if named:
+        return Path(named)
     try:
-        return Path.home() / ".cache" / "chess_transformer" / "int8"
+        home = Path.home()
     except RuntimeError:
         return None
+    return home / ".cache" / "chess_transformer" / "int8"
 
 
 CACHE = cache_folder()
-# these name the cached file (with the rounding code's VERSION): the reference's production values
+# The rounding settings. With VERSION (of the rounding code) and, for a choice of fp16 blocks, CHOICE_VERSION, they name
+# the cached file, in this order; the values are the reference's production ones.
 VERSION = 1
 CALIBRATION_POSITIONS = 1024
 CALIBRATION_FIRST_GAME = 1000
@@ -53,121 +56,133 @@ CALIBRATION_STEP = 9
 DAMPENING = 0.01
 GPTQ_COLUMNS = 128
 FP16_LAST_LAYERS = 1
-INT8_MAX = 127
 CHOICE_VERSION = 1
+INT8_MAX = 127
 ERROR_BATCH = 256
 
 
-def calibration_positions():
-    """Every CALIBRATION_STEP-th position of the Carlsen games after the first CALIBRATION_FIRST_GAME (reference :53-68)."""
-    try:
-        import chess.pgn
-    except ImportError as error:
-        raise ImportError("the calibration positions are read with python-chess; pass encoded boards instead") from error
-    boards = []
-    with open(CARLSEN_PGN) as pgn:
-        for _ in range(CALIBRATION_FIRST_GAME):
-            chess.pgn.skip_game(pgn)
-        while len(boards) < CALIBRATION_POSITIONS and (game := chess.pgn.read_game(pgn)) is not None:
-            board = game.board()
-            for ply, move in enumerate(game.mainline_moves()):
-                board.push(move)
-                if board.is_game_over() or len(boards) == CALIBRATION_POSITIONS:
-                    break
-                if ply % CALIBRATION_STEP == CALIBRATION_STEP // 2:
-                    boards.append(board.copy(stack=False))
-    if len(boards) < CALIBRATION_POSITIONS:
-        raise ValueError(f"{CARLSEN_PGN} has {len(boards)} calibration positions past game {CALIBRATION_FIRST_GAME}, not {CALIBRATION_POSITIONS}")
-    return boards
-
-
-def gptq(weight: torch.Tensor, hessian: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """(int8 weight, f32 scale a row) of an N x K weight: columns rounded in order, each one's rounding error carried
-    onto the columns not yet rounded through the inverse Hessian's upper Cholesky factor (GPTQ). float64 throughout,
-    so that machines summing in other orders round every weight alike."""
-    weight, hessian = weight.double().clone(), hessian.double().clone()
-    columns = weight.shape[1]
-    curvature = hessian.diagonal()
-    # inputs that are always zero (down's padding) have no curvature: their weights stay zero
-    never = curvature == 0
-    curvature[never] = 1
-    weight[:, never] = 0
-    curvature += DAMPENING * curvature.mean()
-    factor = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(hessian)), upper=True)
-    scale = weight.abs().amax(dim=1).clamp(min=1e-20) / INT8_MAX
-    integers = torch.zeros_like(weight)
-    for first in range(0, columns, GPTQ_COLUMNS):
-        last = min(first + GPTQ_COLUMNS, columns)
-        part, part_factor = weight[:, first:last].clone(), factor[first:last, first:last]
-        carried = torch.zeros_like(part)
-        for i in range(last - first):
-            rounded = (part[:, i] / scale).round().clamp(-INT8_MAX, INT8_MAX)
-            integers[:, first + i] = rounded
-            carried[:, i] = (part[:, i] - rounded * scale) / part_factor[i, i]
-            part[:, i:] -= carried[:, i, None] * part_factor[i, i:]
-        weight[:, last:] -= carried @ factor[first:last, last:]
-    return integers.to(torch.int8), scale.float()
+def _row_scales(weight: torch.Tensor) -> torch.Tensor:
+    return weight.abs().amax(dim=1).clamp(min=1e-20) / INT8_MAX
 
 
 def nearest(weight: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """Round to nearest with a scale a row: gptq's answer for a diagonal Hessian, without its column loop."""
+    """(int8, f32 scale a row): each row rounded to nearest on the grid of its absmax / 127, in float64."""
     weight = weight.double()
-    scale = weight.abs().amax(dim=1).clamp(min=1e-20) / INT8_MAX
-    return (weight / scale[:, None]).round().clamp(-INT8_MAX, INT8_MAX).to(torch.int8), scale.float()
+    scale = _row_scales(weight)
+    return torch.round(weight / scale[:, None]).clamp(-INT8_MAX, INT8_MAX).to(torch.int8), scale.float()
+
+
+def gptq(weight: torch.Tensor, hessian: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(int8, f32 scale a row) of an N x K weight by GPTQ, in float64.
+
+    The inputs are rounded one at a time, in order. With U the upper Cholesky factor of the dampened Hessian's inverse, the
+    rounding error of input j, scaled as e_j = (w_j - q_j s) / U[j, j], moves every later input i by -e_j U[j, i], which
+    is the least-squares correction on the calibration inputs. Within a block of GPTQ_COLUMNS inputs each input gathers its
+    corrections from the block's earlier errors when its turn comes (E[:, :j] @ U[:j, j]); a finished block's errors move
+    all later blocks at once. Inputs that are always zero (down's padding) have no curvature: their weights are zero and
+    stay zero."""
+    W = weight.double().clone()
+    H = hessian.double().clone()
+    columns = W.shape[1]
+    curvature = H.diagonal()
+    dead = curvature == 0
+    curvature[dead] = 1.0
+    W[:, dead] = 0.0
+    curvature += DAMPENING * curvature.mean()
+    U = torch.linalg.cholesky(torch.cholesky_inverse(torch.linalg.cholesky(H)), upper=True)
+    scale = _row_scales(W)
+    integers = torch.empty_like(W)
+    for start in range(0, columns, GPTQ_COLUMNS):
+        stop = min(start + GPTQ_COLUMNS, columns)
+        block, factor = W[:, start:stop], U[start:stop, start:stop]
+        errors = torch.zeros_like(block)
+        for j in range(stop - start):
+            corrected = block[:, j] - errors[:, :j] @ factor[:j, j]
+            rounded = torch.round(corrected / scale).clamp(-INT8_MAX, INT8_MAX)
+            integers[:, start + j] = rounded
+            errors[:, j] = (corrected - rounded * scale) / factor[j, j]
+        W[:, stop:] -= errors @ U[start:stop, stop:]
+    return integers.to(torch.int8), scale.float()
+
+
+class HessianRecorder:
+    """While open, sums x^T x in float64 over the inputs x of each block's three int8 matmuls: the projection (Q's input,
+    which K, V and template_mix share), gate_up (the gate's input, which up shares) and down."""
+
+    MATMULS = {"projection": lambda block: block.Q, "gate_up": lambda block: block.mlp.gate_projection, "down": lambda block: block.mlp.down_projection}
+
+    def __init__(self, model: ChessTransformer):
+        self.model = model
+        self.sums: list[dict[str, torch.Tensor]] = [{} for _ in model.encoder]
+        self.hooks = []
+
+    def __enter__(self) -> "HessianRecorder":
+        for sums, block in zip(self.sums, self.model.encoder):
+            for name, layer in self.MATMULS.items():
+                self.hooks.append(layer(block).register_forward_pre_hook(self._adder(sums, name)))
+        return self
+
+    @staticmethod
+    def _adder(sums: dict, name: str):
+        def add(module, inputs):
+            rows = inputs[0].reshape(-1, inputs[0].shape[-1]).double()
+            product = rows.t() @ rows
+            sums[name] = product if name not in sums else sums[name] + product
+        return add
+
+    def __exit__(self, *exception) -> None:
+        for hook in self.hooks:
+            hook.remove()
+        self.hooks.clear()
 
 
 @torch.no_grad()
 def input_hessians(model: ChessTransformer, boards: torch.Tensor, batch: int = 128) -> list[dict[str, torch.Tensor]]:
-    """Per block, the sum over the boards of x^T x of the inputs x of its projection, gate_up and down matmuls."""
-    hessians: list[dict[str, torch.Tensor]] = [{} for _ in model.encoder]
-    hooks = []
-    for block, sums in zip(model.encoder, hessians):
-        for name, layer in (("projection", block.Q), ("gate_up", block.mlp.gate_projection), ("down", block.mlp.down_projection)):
-            def add(module, inputs, name=name, sums=sums):
-                x = inputs[0].reshape(-1, inputs[0].shape[-1])
-                sums[name] = sums.get(name, 0) + x.t() @ x
-            hooks.append(layer.register_forward_pre_hook(add))
-    try:
-        for start in range(0, len(boards), batch):
-            model(boards[start:start + batch].to(model.position_embed.device))
-    finally:
-        for hook in hooks:
-            hook.remove()
-    return hessians
+    """Per block, {matmul: the sum over boards of x^T x of that matmul's inputs}."""
+    device = model.position_embed.device
+    with HessianRecorder(model) as recorder:
+        for part in boards.split(batch):
+            model(part.to(device))
+    return recorder.sums
 
 
 def block_matrices(block) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
-    """A block's projection and gate_up weights, its down weight padded and rotated, and that rotation."""
-    projection = torch.cat([matmul.weight for matmul in (block.Q, block.K, block.V, block.template_mix)])
+    """A block's projection and gate_up weights as Int8Block reads them, its down weight padded to down_inputs(hidden) and
+    rotated by the block-diagonal Hadamard matrix / 32, and that rotation."""
+    down = block.mlp.down_projection.weight
+    width = down_inputs(down.shape[1])
+    rotation = torch.kron(torch.eye(width // HADAMARD_BLOCK), hadamard(HADAMARD_BLOCK)).to(down)
+    projection = torch.cat([block.Q.weight, block.K.weight, block.V.weight, block.template_mix.weight])
     gate_up = torch.cat([block.mlp.gate_projection.weight, block.mlp.up_projection.weight])
-    hidden = block.mlp.down_projection.weight.shape[1]
-    width = down_inputs(hidden)
-    rotation = torch.block_diag(*[hadamard(HADAMARD_BLOCK)] * (width // HADAMARD_BLOCK)).to(block.mlp.down_projection.weight)
-    down = nn.functional.pad(block.mlp.down_projection.weight, (0, width - hidden)) @ rotation / HADAMARD_BLOCK
-    return projection, gate_up, down, rotation
+    rotated = nn.functional.pad(down, (0, width - down.shape[1])) @ rotation / HADAMARD_BLOCK
+    return projection, gate_up, rotated, rotation
+
+
+def int8_layers(model: ChessTransformer) -> range:
+    return range(len(model.encoder) - FP16_LAST_LAYERS)
 
 
 @torch.no_grad()
 def compute_int8_weights(model: ChessTransformer, boards: torch.Tensor) -> Int8Weights:
-    """All but the last FP16_LAST_LAYERS blocks, GPTQ-rounded on the Hessians of boards (reference :124-140)."""
+    """GPTQ on the calibration boards' Hessians, for all but the last FP16_LAST_LAYERS blocks (reference :124-140). down's
+    Hessian is of its rotated inputs: R^T H R over the zero-padded hidden units."""
     hessians = input_hessians(model, boards)
     weights = {}
-    for layer in range(len(hessians) - FP16_LAST_LAYERS):
-        block, sums = model.encoder[layer], hessians[layer]
-        projection, gate_up, down, rotation = block_matrices(block)
+    for layer in int8_layers(model):
+        projection, gate_up, down, rotation = block_matrices(model.encoder[layer])
+        sums = hessians[layer]
         padding = rotation.shape[0] - sums["down"].shape[0]
-        padded = nn.functional.pad(sums["down"], (0, padding, 0, padding))
-        weights[layer] = {"projection": gptq(projection, sums["projection"]), "gate_up": gptq(gate_up, sums["gate_up"]),
-                          "down": gptq(down, rotation.t() @ padded @ rotation)}
+        rotated = rotation.t() @ nn.functional.pad(sums["down"], (0, padding, 0, padding)) @ rotation
+        weights[layer] = {"projection": gptq(projection, sums["projection"]), "gate_up": gptq(gate_up, sums["gate_up"]), "down": gptq(down, rotated)}
     return weights
 
 
 @torch.no_grad()
 def nearest_int8_weights(model: ChessTransformer) -> Int8Weights:
-    """compute_int8_weights with diagonal Hessians -- round to nearest, same layout -- for random-init networks that have no
-    calibration positions worth the name (the benchmarks' networks)."""
+    """compute_int8_weights with diagonal Hessians -- round to nearest, the same layout -- for random-init networks, which
+    have no calibration positions worth the name (the tests' and the benchmark's)."""
     weights = {}
-    for layer in range(len(model.encoder) - FP16_LAST_LAYERS):
+    for layer in int8_layers(model):
         projection, gate_up, down, _ = block_matrices(model.encoder[layer])
         weights[layer] = {"projection": nearest(projection), "gate_up": nearest(gate_up), "down": nearest(down)}
     return weights
@@ -175,107 +190,129 @@ def nearest_int8_weights(model: ChessTransformer) -> Int8Weights:
 
 @torch.no_grad()
 def block_errors(checkpoint_path: Path, weights: Int8Weights, boards: torch.Tensor | None = None, legal: torch.Tensor | None = None) -> dict[int, float]:
-    """Per layer of weights, the policy's total variation over the legal moves between the fp16 model and the fp16 model with only
-    that block in int8, mean over the calibration boards (reference :145-170). Without python-chess, pass boards and their
-    legal-move masks (B x 1968 bool) -- or boards alone to take every move as legal."""
+    """Per layer of weights: the total variation distance between the policy over the legal moves of the fp16 network and
+    of the fp16 network with that one block in int8, mean over the calibration boards (reference :145-170). Without
+    python-chess pass the boards and their legal-move masks (B x 1968), or the boards alone to count every move legal."""
     from engine.inference import FP16_RESIDUAL_SCALE, answer_rows, fp16_model
     if boards is None:
         boards, legal = encoded_calibration()
     device = torch.device("cuda")
     boards = boards.to(device)
-    legal = torch.ones(len(boards), answer_rows_width(checkpoint_path) - 1, dtype=torch.bool, device=device) if legal is None else legal.to(device)
     model = fp16_model(checkpoint_path)
-    fp16_blocks = list(model.encoder)
+    originals = list(model.encoder)
 
-    def priors(int8_blocks: dict[int, nn.Module]) -> torch.Tensor:
-        blocks = [int8_blocks.get(layer, block) for layer, block in enumerate(fp16_blocks)]
+    def policy(replaced: dict[int, nn.Module]) -> torch.Tensor:
+        blocks = [replaced.get(layer, block) for layer, block in enumerate(originals)]
         link_input_mixes(blocks)
         model.encoder = nn.ModuleList(blocks)
-        logits = torch.cat([answer_rows(model(boards[start:start + ERROR_BATCH]))[:, :-1] for start in range(0, len(boards), ERROR_BATCH)])
-        return torch.softmax(logits.double().masked_fill(~legal, -torch.inf), dim=-1)
+        logits = torch.cat([answer_rows(model(part))[:, :-1] for part in boards.split(ERROR_BATCH)]).double()
+        if legal is not None:
+            logits = logits.masked_fill(~legal.to(device), -torch.inf)
+        return torch.softmax(logits, dim=-1)
 
-    fp16_priors = priors({})
-    errors = {}
-    for layer, matmuls in weights.items():
-        int8_priors = priors({layer: Int8Block(fp16_blocks[layer], matmuls, FP16_RESIDUAL_SCALE)})
-        errors[layer] = 0.5 * (int8_priors - fp16_priors).abs().sum(dim=-1).mean().item()
+    baseline = policy({})
+    errors = {layer: 0.5 * (policy({layer: Int8Block(originals[layer], matmuls, FP16_RESIDUAL_SCALE)}) - baseline).abs().sum(-1).mean().item()
+              for layer, matmuls in weights.items()}
     del model
     torch.cuda.empty_cache()
     return errors
 
 
-def answer_rows_width(checkpoint_path: Path) -> int:
-    from model.encoding import NUM_MOVE_IDS
-    return NUM_MOVE_IDS + 1
+def calibration_positions():
+    """Every CALIBRATION_STEP-th position (from the middle of each step) of the Carlsen games from game CALIBRATION_FIRST_GAME
+    on, until CALIBRATION_POSITIONS: python-chess boards (reference :53-68)."""
+    try:
+        import chess.pgn
+    except ImportError as error:
+        raise ImportError("the calibration positions are read with python-chess; pass encoded boards instead") from error
+    positions = []
+    with open(CARLSEN_PGN) as pgn:
+        for _ in range(CALIBRATION_FIRST_GAME):
+            chess.pgn.skip_game(pgn)
+        while len(positions) < CALIBRATION_POSITIONS:
+            game = chess.pgn.read_game(pgn)
+            if game is None:
+                break
+            board = game.board()
+            for ply, move in enumerate(game.mainline_moves()):
+                board.push(move)
+                if board.is_game_over() or len(positions) == CALIBRATION_POSITIONS:
+                    break
+                if ply % CALIBRATION_STEP == CALIBRATION_STEP // 2:
+                    positions.append(board.copy(stack=False))
+    if len(positions) < CALIBRATION_POSITIONS:
+        raise ValueError(f"{CARLSEN_PGN} has {len(positions)} calibration positions past game {CALIBRATION_FIRST_GAME}, not {CALIBRATION_POSITIONS}")
+    return positions
+
+
+def board_tokens(board) -> list[int]:
+    """A python-chess board as the network's 70 tokens, seen from the side to move (the layout of model/encoding.py)."""
+    import chess
+    from model.encoding import CASTLING_TOKEN_OFFSET, EN_PASSANT_TOKEN_OFFSET, NUM_PIECE_TYPES, TURN_TOKEN_OFFSET
+    mover = board.turn
+    mirror = 0 if mover == chess.WHITE else 56
+    tokens = [0] * 64
+    for square, piece in board.piece_map().items():
+        tokens[square ^ mirror] = piece.piece_type + (0 if piece.color == mover else NUM_PIECE_TYPES)
+    rights = [board.has_kingside_castling_rights(mover), board.has_queenside_castling_rights(mover),
+              board.has_kingside_castling_rights(not mover), board.has_queenside_castling_rights(not mover)]
+    passing = board.ep_square ^ mirror if board.ep_square is not None and board.has_legal_en_passant() else 0
+    return tokens + [TURN_TOKEN_OFFSET + int(mover == chess.WHITE)] + [CASTLING_TOKEN_OFFSET + int(right) for right in rights] \
+        + [EN_PASSANT_TOKEN_OFFSET + passing]
 
 
 def encoded_calibration() -> tuple[torch.Tensor, torch.Tensor]:
-    """The calibration positions encoded, with their legal-move masks (python-chess)."""
-    positions = calibration_positions()
+    """The calibration positions' tokens and legal-move masks (python-chess)."""
+    import chess
     from model.encoding import NUM_MOVE_IDS, move_id
-    import chess
-    tokens, legal = [], torch.zeros(len(positions), NUM_MOVE_IDS, dtype=torch.bool)
+    positions = calibration_positions()
+    legal = torch.zeros(len(positions), NUM_MOVE_IDS, dtype=torch.bool)
     for row, board in enumerate(positions):
-        tokens.append(encode_board(board))
-        promotion = lambda move: move.promotion
-        legal[row, [move_id(move.from_square, move.to_square, promotion(move), board.turn == chess.WHITE) for move in board.legal_moves]] = True
-    return torch.tensor(tokens, dtype=torch.long), legal
+        for move in board.legal_moves:
+            legal[row, move_id(move.from_square, move.to_square, move.promotion, board.turn == chess.WHITE)] = True
+    return torch.tensor([board_tokens(board) for board in positions], dtype=torch.long), legal
 
 
-def encode_board(board) -> list[int]:
-    """A python-chess board as its 70 tokens, seen from the side to move (reference model/encoding.py:72-92)."""
-    import chess
-    from model.encoding import CASTLING_TOKEN_OFFSET, EN_PASSANT_TOKEN_OFFSET, NUM_PIECE_TYPES, TURN_TOKEN_OFFSET
-    turn, opponent = board.turn, not board.turn
-    flip = 0 if turn == chess.WHITE else 56
-    tokens = [0] * 64
-    for piece_type in chess.PIECE_TYPES:
-        for square in chess.scan_forward(board.pieces_mask(piece_type, turn)):
-            tokens[square ^ flip] = piece_type
-        for square in chess.scan_forward(board.pieces_mask(piece_type, opponent)):
-            tokens[square ^ flip] = piece_type + NUM_PIECE_TYPES
-    en_passant = board.ep_square ^ flip if board.ep_square is not None and board.has_legal_en_passant() else 0
-    return tokens + [TURN_TOKEN_OFFSET + (1 if turn == chess.WHITE else 0),
-                     CASTLING_TOKEN_OFFSET + int(board.has_kingside_castling_rights(turn)),
-                     CASTLING_TOKEN_OFFSET + int(board.has_queenside_castling_rights(turn)),
-                     CASTLING_TOKEN_OFFSET + int(board.has_kingside_castling_rights(opponent)),
-                     CASTLING_TOKEN_OFFSET + int(board.has_queenside_castling_rights(opponent)),
-                     EN_PASSANT_TOKEN_OFFSET + en_passant]
+def rounding_settings(fp16_blocks: int) -> tuple:
+    settings = (VERSION, CALIBRATION_POSITIONS, CALIBRATION_FIRST_GAME, CALIBRATION_STEP, DAMPENING, GPTQ_COLUMNS, FP16_LAST_LAYERS,
+                HADAMARD_BLOCK, DOWN_INPUT_MULTIPLE)
+    return settings + (CHOICE_VERSION, fp16_blocks) if fp16_blocks else settings
 
 
 def cached_weights_path(checkpoint_path: Path, fp16_blocks: int) -> Path | None:
-    """CACHE / "<sha256 of the checkpoint>_<sha256 of the rounding settings, 16 hex>.pt"; a count of 0 stays out of the name."""
+    """CACHE / "<checkpoint sha256>_<16 hex digits of the rounding settings' sha256>.pt"; a count of 0 stays out of the
+    settings, so that files cached before the count existed are read. None without a cache folder."""
     if CACHE is None:
         return None
+    content = hashlib.sha256()
     with open(checkpoint_path, "rb") as checkpoint:
-        digest = hashlib.file_digest(checkpoint, "sha256").hexdigest() if hasattr(hashlib, "file_digest") else hashlib.sha256(checkpoint.read()).hexdigest()
-    rounding = (VERSION, CALIBRATION_POSITIONS, CALIBRATION_FIRST_GAME, CALIBRATION_STEP, DAMPENING, GPTQ_COLUMNS, FP16_LAST_LAYERS,
-                HADAMARD_BLOCK, DOWN_INPUT_MULTIPLE)
-    if fp16_blocks:
-        rounding += (CHOICE_VERSION, fp16_blocks)
-    return CACHE / f"{digest}_{hashlib.sha256(repr(rounding).encode()).hexdigest()[:16]}.pt"
+        for chunk in iter(lambda: checkpoint.read(1 << 20), b""):
+            content.update(chunk)
+    settings = hashlib.sha256(repr(rounding_settings(fp16_blocks)).encode()).hexdigest()[:16]
+    return CACHE / f"{content.hexdigest()}_{settings}.pt"
 
 
 def int8_weights(checkpoint_path: Path, fp16_blocks: int, boards: torch.Tensor | None = None, legal: torch.Tensor | None = None) -> Int8Weights:
-    """The checkpoint's int8 weights on the cpu, from CACHE or computed on the gpu and cached, without the fp16_blocks blocks of the
-    largest block_errors (reference :188-207). boards (and legal) replace the calibration positions where python-chess is absent."""
+    """The checkpoint's int8 weights on the CPU: read from CACHE, or computed on the GPU and cached. fp16_blocks: the blocks
+    of the largest block_errors kept out (reference :188-207). boards (and legal) stand in for the calibration positions
+    where python-chess is absent."""
     if fp16_blocks < 0:
         raise ValueError(f"a count of blocks to keep in fp16, not {fp16_blocks}")
     path = cached_weights_path(checkpoint_path, fp16_blocks)
     if path is not None and path.exists():
         return torch.load(path, weights_only=True)
     if fp16_blocks:
-        weights = int8_weights(checkpoint_path, 0, boards, legal)
-        errors = block_errors(checkpoint_path, weights, boards, legal)
-        kept = sorted(errors, key=errors.get, reverse=True)[:fp16_blocks]
-        weights = {layer: matmuls for layer, matmuls in weights.items() if layer not in kept}
+        every = int8_weights(checkpoint_path, 0, boards, legal)
+        errors = block_errors(checkpoint_path, every, boards, legal)
+        worst = set(sorted(errors, key=errors.get, reverse=True)[:fp16_blocks])
+        weights = {layer: matmuls for layer, matmuls in every.items() if layer not in worst}
     else:
         if boards is None:
             boards, _ = encoded_calibration()
-        #fp64 but the heads, whose inputs the model casts to fp32
+        # float64 throughout but the heads, whose inputs the model casts to f32
         model = load_model(checkpoint_path, torch.device("cuda")).half_except_heads(torch.float64)
-        weights = {layer: {name: tuple(tensor.cpu() for tensor in pair) for name, pair in matmuls.items()}
-                   for layer, matmuls in compute_int8_weights(model, boards).items()}
+        computed = compute_int8_weights(model, boards)
+        weights = {layer: {name: (integers.cpu(), scale.cpu()) for name, (integers, scale) in matmuls.items()} for layer, matmuls in computed.items()}
         del model
         torch.cuda.empty_cache()
     cache_weights(weights, path)
@@ -283,34 +320,42 @@ def int8_weights(checkpoint_path: Path, fp16_blocks: int, boards: torch.Tensor |
 
 
 def cache_weights(weights: Int8Weights, path: Path | None) -> None:
-    """Written under another name first, then moved: engines starting together compute the same weights."""
+    """Saves weights at path by way of a file of this process's own, renamed into place, so that engines starting together
+    never read half a file. A cache that cannot be written is reported and costs only the next start's time."""
     if path is None:
-        print("the int8 weights are not cached: there is no home folder", file=sys.stderr)
+        print("the int8 weights are not cached: there is no cache folder (no home folder and no $" + CACHE_VARIABLE + ")", file=sys.stderr)
         return
-    partial = path.with_name(f"{path.name}.{os.getpid()}.partial")
+    staging = path.parent / f".{path.name}.{os.getpid()}"
     try:
         path.parent.mkdir(parents=True, exist_ok=True)
-        torch.save(weights, partial)
-        os.replace(partial, path)
+        torch.save(weights, staging)
+        os.replace(staging, path)
     except (OSError, RuntimeError) as error:
-        with suppress(OSError):
-            partial.unlink()
-        print(f"the int8 weights are not cached: {error}", file=sys.stderr)
+        try:
+            staging.unlink()
+        except OSError:
+            pass
+        print(f"the int8 weights are not cached at {path}: {error}", file=sys.stderr)
+
+
+def main(arguments: list[str] | None = None) -> int:
+    parser = argparse.ArgumentParser(description="compute a checkpoint's int8 weights and write them to the cache the engine reads")
+    parser.add_argument("checkpoint", type=Path)
+    parser.add_argument("--fp16-blocks", type=int, default=1, help="blocks besides the last to keep in fp16 (the engine's ENGINE_FP16_BLOCKS)")
+    parser.add_argument("--path", action="store_true", help="only print where the cached file is or would be (no GPU needed)")
+    options = parser.parse_args(arguments)
+    path = cached_weights_path(options.checkpoint, options.fp16_blocks)
+    if options.path or path is None:
+        print(path if path is not None else f"no cache folder: set ${CACHE_VARIABLE}", file=sys.stdout if path else sys.stderr)
+        return 0 if path is not None else 1
+    weights = int8_weights(options.checkpoint, options.fp16_blocks)
+    if not path.exists():
+        print(f"computed, but {path} could not be written: the engine would compute the weights again at its start", file=sys.stderr)
+        return 1
+    print(path)
+    print("int8 blocks:", sorted(weights))
+    return 0
 
 
 if __name__ == "__main__":
-    parser = argparse.ArgumentParser(description="the int8 weights of a checkpoint, computed and cached")
-    parser.add_argument("checkpoint", type=Path)
-    parser.add_argument("--fp16-blocks", type=int, default=1, help="blocks kept in fp16 besides the last (the engine's ENGINE_FP16_BLOCKS)")
-    parser.add_argument("--path", action="store_true", help="print the cached file's path and stop: nothing is computed, and no gpu is needed")
-    arguments = parser.parse_args()
-    path = cached_weights_path(arguments.checkpoint, arguments.fp16_blocks)
-    if arguments.path:
-        if path is None:
-            raise SystemExit("the int8 weights have no cached file: there is no home folder")
-        print(path)
-        raise SystemExit
-    weights = int8_weights(arguments.checkpoint, arguments.fp16_blocks)
-    if path is None or not path.exists():
-        raise SystemExit("the int8 weights could not be cached, which is what this is for: the engine would compute them at its first isready")
-    print(path)
+    sys.exit(main())

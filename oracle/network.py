@@ -85,6 +85,49 @@ def square_feature_rows(boards: np.ndarray) -> np.ndarray:
     return rows
 
 
+def _board_tables():
+    """Per square: its 8 neighbours, its 8 rays of 7 squares (nearest first) and its 8 knight jumps, 64 standing for off the
+    board; and each square's rank and file."""
+    step = lambda s, df, dr: (s // 8 + dr) * 8 + s % 8 + df if _on_board(s % 8 + df, s // 8 + dr) else 64
+    rays = np.array([[[step(s, df * k, dr * k) for k in range(1, 8)] for df, dr in DIRECTIONS] for s in range(NUM_SQUARES)])
+    jumps = np.array([[step(s, df, dr) for df, dr in KNIGHT_JUMPS] for s in range(NUM_SQUARES)])
+    return rays, jumps, np.arange(NUM_SQUARES) // 8, np.arange(NUM_SQUARES) % 8
+
+
+RAYS, JUMPS, RANKS, FILES = _board_tables()
+
+
+def _first(found: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """Over the last axis: whether found holds anywhere, and the first place it does (0 if nowhere)."""
+    return found.any(-1), found.argmax(-1)
+
+
+def square_feature_rows_fast(boards: np.ndarray) -> np.ndarray:
+    """square_feature_rows for many boards at once, with numpy array operations (the CPU baseline's forward); the same rows
+    (tests/test_oracle.py checks the two against each other)."""
+    squares = np.asarray(boards)[:, :NUM_SQUARES].astype(np.int64)
+    B = len(squares)
+    padded = np.concatenate([squares, np.full((B, 1), EDGE)], 1)
+    rows = np.zeros((B, NUM_SQUARES, 23), dtype=np.int64)
+    for slot, code in enumerate((KING, KING + THEIRS, QUEEN, QUEEN + THEIRS)):
+        present, where = _first(squares == code)
+        offset = (RANKS[None, :] - RANKS[where][:, None] + 7) * 15 + FILES[None, :] - FILES[where][:, None] + 7
+        rows[..., slot] = np.where(present[:, None], offset, NO_PIECE)
+    along = padded[:, RAYS]                                       # B x 64 x 8 x 7
+    rows[..., 4:12] = along[..., 0]
+    present, where = _first((along != 0) & (along != EDGE))
+    first = np.take_along_axis(along, where[..., None], -1)[..., 0]
+    rows[..., 12:20] = np.where(present, 1 + (first - 1) * 7 + where, 0)
+    jumps = padded[:, JUMPS]
+    rows[..., 20] = np.minimum((jumps == KNIGHT).sum(-1), 2) * 3 + np.minimum((jumps == KNIGHT + THEIRS).sum(-1), 2)
+    for slot, direction in ((21, 0), (22, 1)):                     # up and down the file: the first pawn, past any piece
+        file_ray = along[:, :, direction]
+        present, where = _first((file_ray == PAWN) | (file_ray == PAWN + THEIRS))
+        pawn = np.take_along_axis(file_ray, where[..., None], -1)[..., 0]
+        rows[..., slot] = np.where(present, 1 + (pawn == PAWN + THEIRS) * 7 + where, 0)
+    return rows
+
+
 def _tensor(state: dict, name: str, dtype=torch.float64) -> torch.Tensor:
     return state[name].detach().cpu().to(dtype)
 
@@ -98,7 +141,7 @@ def _layers(state: dict) -> int:
 
 
 def _embedding(state: dict, boards: torch.Tensor, dtype) -> torch.Tensor:
-    features = torch.from_numpy(square_feature_rows(boards.numpy()) + ROW_OFFSETS)
+    features = torch.from_numpy(square_feature_rows_fast(boards.numpy()) + ROW_OFFSETS)
     table = _tensor(state, "square_features.table", dtype)
     summed = table[features].sum(-2)
     embed = _tensor(state, "embed.weight", dtype)[boards] + _tensor(state, "position_embed", dtype)

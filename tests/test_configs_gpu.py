@@ -1,0 +1,107 @@
+"""BASELINE's network configs on the GPU, on seeded random legal positions (tests/golden/positions.npz):
+
+- config 3/4, the benchmarked d512 x 28 int8 network exactly as bench.py builds it, against the north star's bars on
+  1,024 positions (logits within 2e-2 max-abs, the same argmax move on at least 99.9% of positions, value within 5e-3),
+  the expected outputs computed by the CPU oracle in a fixture (tests/golden/make_network_outputs.py);
+- the same network's answer rows at batches 2, 1,024 and 4,096 through HIP graphs, bit for bit the same for a position
+  wherever it sits in the batch (every tile, row-kernel launch and attention run the batch sizes pick);
+- config 0, the d256 x 4 network (8 heads, SwiGLU 1024), against the oracle on 64 positions."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from bench import SETTINGS, legal_boards, synthetic_model
+from engine.inference import answer_rows, int8_network
+from engine.quantization import nearest_int8_weights
+from model.model import expected_score
+from oracle import network as oracle_network
+
+pytestmark = pytest.mark.gpu
+
+FIXTURE = Path(__file__).resolve().parent / "golden" / "network_d512x28.npz"
+CONFIG0 = {"d_model": 256, "num_layers": 4, "n_heads": 8, "kv_heads": 8, "mlp_hidden": 1024, "value_bins": 128, "position_templates": 8}
+
+
+def graphed_rows(network, boards: torch.Tensor) -> torch.Tensor:
+    """The network's answer rows for boards, from a HIP graph recorded at their batch and replayed twice on its own stream."""
+    device = next(network.parameters()).device
+    stream = torch.cuda.Stream(device)
+    inputs = boards.to(device)
+    stream.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(stream), torch.no_grad():
+        network(inputs)
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream), torch.no_grad():
+        rows = answer_rows(network(inputs))
+    replays = []
+    for _ in range(2):
+        with torch.cuda.stream(stream):
+            graph.replay()
+        torch.cuda.synchronize(device)
+        replays.append(rows.cpu())
+    assert torch.equal(replays[0], replays[1])
+    del graph
+    return replays[0]
+
+
+@pytest.fixture(scope="module")
+def benchmarked():
+    model = synthetic_model(SETTINGS, 0)
+    weights = nearest_int8_weights(model)
+    return int8_network(model.to(torch.device("cuda", torch.cuda.current_device())), weights)
+
+
+def check_bars(logits: torch.Tensor, values: torch.Tensor, expected_logits: torch.Tensor, expected_values: torch.Tensor, scores=None):
+    """The north star's bars: logits within 2e-2 max-abs, argmax equal on >= 99.9%, value within 5e-3."""
+    assert (logits - expected_logits).abs().max() < 2e-2
+    agree = (logits.argmax(-1) == expected_logits.argmax(-1)).double().mean()
+    assert agree >= 0.999
+    if values is not None:
+        assert (values - expected_values).abs().max() < 5e-3
+    found_scores = expected_score(values) if scores is None else scores
+    assert (found_scores - expected_score(expected_values)).abs().max() < 5e-3
+
+
+def test_the_benchmarked_network_meets_the_bars_on_1024_positions(benchmarked):
+    data = np.load(FIXTURE)
+    boards = torch.from_numpy(data["boards"].astype(np.int64))
+    assert torch.equal(boards, legal_boards(len(boards)))
+    expected_logits, expected_values = torch.from_numpy(data["logits"]), torch.from_numpy(data["value_logits"])
+    rows = graphed_rows(benchmarked, boards)
+    check_bars(rows[:, :-1], None, expected_logits, expected_values, scores=rows[:, -1])
+    benchmarked.fused_heads = False
+    try:
+        with torch.no_grad():
+            logits, values = benchmarked(boards.to(next(benchmarked.parameters()).device))
+    finally:
+        benchmarked.fused_heads = True
+    assert torch.equal(logits.cpu(), rows[:, :-1])
+    check_bars(logits.cpu(), values.cpu(), expected_logits, expected_values)
+
+
+def test_a_positions_answer_does_not_depend_on_its_batch(benchmarked):
+    """Batches of 4,096 and 1,024 (the bench's largest and its throughput batch: 286,720 and 71,680 rows, the row kernels'
+    wide launches, the big GEMM tiles) and of 2 (the small tiles), through graphs: a position's answer row is the same
+    bits wherever it sits, the first, a middle and the last row tile of the big batch included."""
+    boards = legal_boards(4096)
+    largest = graphed_rows(benchmarked, boards)
+    assert torch.equal(graphed_rows(benchmarked, boards[:1024]), largest[:1024])
+    for slots in ([0, 1], [2047, 2048], [4094, 4095], [5, 3000]):
+        assert torch.equal(graphed_rows(benchmarked, boards[slots]), largest[slots]), slots
+
+
+def test_config0_the_d256_network_is_the_oracles():
+    """BASELINE config 0's network (d256, 4 blocks: 3 int8 and the fp16 last, 8 heads, SwiGLU 1024) on 64 legal positions."""
+    model = synthetic_model(CONFIG0, 1)
+    state = {name: value.clone() for name, value in model.state_dict().items()}
+    weights = nearest_int8_weights(model)
+    boards = legal_boards(64, 2048)
+    network = int8_network(model.to(torch.device("cuda", torch.cuda.current_device())), weights)
+    network.fused_heads = False
+    with torch.no_grad():
+        logits, values = network(boards.to(next(network.parameters()).device))
+    expected_logits, expected_values = oracle_network.int8_forward(state, CONFIG0, weights, boards)
+    check_bars(logits.cpu(), values.cpu(), expected_logits, expected_values)

@@ -51,7 +51,7 @@ def test_norm_quant_matches_the_oracle_to_the_bit(device, D, mix):
 @pytest.mark.parametrize("rows, D", [(210, 128), (210, 192), (210, 512), (210, 768), (40000, 512)])
 @pytest.mark.parametrize("mix", [False, True])
 def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
-    """The fp16 blocks' norm (and their own input mix): the oracle's bits, one and four rows a wavefront (40,000 rows);
+    """The fp16 blocks' norm (and their own input mix): the oracle's bits, one row a wavefront and (40,000 rows) two;
     within one fp16 rounding of torch's rms_norm in f32 (the reference's nn.RMSNorm)."""
     torch.manual_seed(rows + D)
     x = (torch.randn(rows, D, device=device) * 4).half()
@@ -92,7 +92,7 @@ def test_norm_quant_rounds_the_rmsnorm(device):
         assert ((integers.float() * scale[..., None] - normed).abs() <= 0.501 * step[..., None]).all()
 
 
-@pytest.mark.parametrize("hidden, width", [(992, 1024), (320, 384), (2048, 2048), (100, 128)])
+@pytest.mark.parametrize("hidden, width", [(992, 1024), (320, 384), (2048, 2048), (100, 128), (512, 512), (1024, 1024), (1536, 1536)])
 def test_rotate_quant_matches_the_oracle_to_the_bit(device, hidden, width):
     torch.manual_seed(hidden)
     h = torch.randn(3, 70, hidden, device=device).half()
@@ -101,6 +101,39 @@ def test_rotate_quant_matches_the_oracle_to_the_bit(device, hidden, width):
     # a 32-block of padding alone rotates to zeros; a block that holds real columns spreads them over all 32
     padding = -(-hidden // HADAMARD_BLOCK) * HADAMARD_BLOCK
     assert integers.shape == (3, 70, width) and (integers[..., padding:] == 0).all()
+    assert bits_equal(integers, expected_q) and bits_equal(scale, expected_scale)
+
+
+# the network's batch-1024 rows: 1,024 positions of 70 tokens. From 32,768 rows the row kernels take their wide launches
+# (two rows a wavefront, full rows without masks), which only the d512 network's batch-256-and-up shapes reach.
+WIDE_ROWS = 71680
+
+
+@pytest.mark.parametrize("mix", [False, True])
+def test_norm_quant_at_the_batch_1024_rows_is_the_oracles(device, mix):
+    """norm_quant's wide launch (71,680 rows of 512: two rows a wavefront, no masks) against the oracle, to the bit."""
+    generator = torch.Generator(device="cpu").manual_seed(17 + mix)
+    x = (torch.randn(WIDE_ROWS, 512, generator=generator) * 4).half()
+    original = torch.randn(WIDE_ROWS, 512, generator=generator).half()
+    gain = (torch.rand(512, generator=generator) + 0.5).half()
+    rs, is_ = torch.tensor([0.8]).half(), torch.tensor([0.5]).half()
+    if mix:
+        mixed, q, scale = mix_norm_quant(x.to(device), original.to(device), rs.to(device), is_.to(device), gain.to(device), 1e-5)
+        expected_mixed, expected_q, expected_scale = oracle.mix_norm_quant(x.numpy(), original.numpy(), rs.numpy(), is_.numpy(), gain.numpy(), 1e-5)
+        assert bits_equal(mixed, expected_mixed)
+    else:
+        q, scale = norm_quant(x.to(device), gain.to(device), 1e-5)
+        expected_q, expected_scale = oracle.norm_quant(x.numpy(), gain.numpy(), 1e-5)
+    assert bits_equal(q, expected_q) and bits_equal(scale, expected_scale)
+
+
+def test_rotate_quant_at_the_batch_1024_rows_is_the_oracles(device):
+    """rotate_quant's wide launch (71,680 rows of 2,048, the network's down input: two rows a wavefront, full rows without
+    masks, the cross-lane butterflies as signed FMAs) against the oracle, to the bit."""
+    generator = torch.Generator(device="cpu").manual_seed(19)
+    h = torch.randn(WIDE_ROWS, 2048, generator=generator).half()
+    integers, scale = rotate_quant(h.to(device), hadamard(HADAMARD_BLOCK).to(device).half(), 2048)
+    expected_q, expected_scale = oracle.rotate_quant(h.numpy(), 2048)
     assert bits_equal(integers, expected_q) and bits_equal(scale, expected_scale)
 
 
@@ -232,7 +265,38 @@ def test_int8_linear_writes_bf16(device):
     assert np.array_equal(cpu(out.float()), expected)
 
 
-ALL_TILES = (*range(1, 12), 13)   # 12 is the gated-only streamed kernel, tested on its own; 13 takes 128-byte stages
+def config1_case(M: int, K: int, N: int, device):
+    """A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02) (a scale a row), f32 row scales,
+    bias N(0, 0.02), bf16 out."""
+    from engine.quantization import nearest
+    generator = torch.Generator(device="cpu").manual_seed(M + K + N)
+    x = torch.randint(-127, 128, (M, K), generator=generator, dtype=torch.int8)
+    x_scale = torch.rand(M, generator=generator) / 100
+    weight, weight_scale = nearest(torch.randn(N, K, generator=generator) * 0.02)
+    bias = (torch.randn(N, generator=generator) * 0.02).half()
+    return x, x_scale, weight, weight_scale, bias
+
+
+CONFIG1_SHAPES = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]   # QKV, attention-out, FFN-up, FFN-down (K to N)
+
+
+@pytest.mark.parametrize("K, N", CONFIG1_SHAPES, ids=["qkv", "attention_out", "ffn_up", "ffn_down"])
+@pytest.mark.parametrize("M", [4096, 65536])
+def test_the_config1_gemms_are_the_oracles_in_bf16(device, M, K, N):
+    """The four per-layer shapes of BASELINE config 1 with the bias epilogue and bf16 out, the tile the size picks: every row
+    against the oracle at M = 4,096; at M = 65,536 the rows of the first, a middle and the last row tile and 256 rows drawn
+    across the rest (the oracle's integer product of all 65,536 rows takes minutes)."""
+    x, x_scale, weight, weight_scale, bias = config1_case(M, K, N, device)
+    out = launch_int8_linear(x.to(device), x_scale.to(device), weight.to(device), weight_scale.to(device), bias.to(device), None, False,
+                             None, None, None, 0, torch.bfloat16)
+    assert out.dtype == torch.bfloat16 and out.shape == (M, N)
+    rows = np.arange(M) if M <= 4096 else np.unique(np.concatenate([np.arange(256), np.arange(M // 2 - 128, M // 2 + 128), np.arange(M - 256, M),
+                                                                       np.random.default_rng(M + N).integers(0, M, 256)]))
+    expected = oracle.int8_linear(x.numpy()[rows], x_scale.numpy()[rows], weight.numpy(), weight_scale.numpy(), bias.numpy(), out_dtype="bf16")
+    assert np.array_equal(cpu(out.float())[rows], expected)
+
+
+ALL_TILES = (*range(1, 12), 13)   # 12 is not a tile; 13 takes 128-byte stages
 
 
 @pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])

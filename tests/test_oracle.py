@@ -207,6 +207,16 @@ def test_the_square_features_of_a_known_position():
     assert features[A1, 4 + 3] == 13 and features[A1, 12 + 3] == 0
 
 
+def test_the_fast_square_features_are_the_square_by_square_walk():
+    """The array form the CPU forward uses against the square-by-square walk that the known position pins, on boards with
+    every code anywhere (several kings or none, pawns on the edge ranks) and on the known position."""
+    generator = np.random.default_rng(5)
+    boards = generator.integers(0, 13, (300, 70))
+    boards[:40, :64] = generator.choice([0, 0, 0, 1, 7, 2, 8, 5, 11], (40, 64))
+    boards[40] = KNOWN
+    assert np.array_equal(network.square_feature_rows_fast(boards), network.square_feature_rows(boards))
+
+
 def test_the_input_embedding_is_the_models():
     """The slot-order f32 sum of the feature rows, rounded to fp16, plus the token and position embeddings: the model's embedding in
     f64 (model/model.py:245-250 of the reference) to within the fp16 roundings."""
@@ -275,6 +285,44 @@ def test_scaling_the_residual_stream_changes_no_output():
     before = network.fp32_forward({k: v.clone() for k, v in model.state_dict().items()}, SMALL, boards, eps=0.0)
     after = network.fp32_forward(model.scale_residual_stream(1 / 16).state_dict(), SMALL, boards, eps=0.0)
     assert all(torch.allclose(a, b, atol=1e-4) for a, b in zip(before, after))
+
+
+def test_a_block_with_uniform_attention_adds_the_mean_value_row():
+    """A closed form of one block: with Q's and K's weights and biases zero and no template bias the scores are all equal, so
+    every token attends to the mean of the 70 value rows; with the mlp's down weight zero and the input unmixed (residual
+    scale 1, input scale 0) the block adds combine_heads(mean V) to its input. The oracle's forward of such a one-block
+    model equals the heads of the final norm of embedding + that row, computed here from the state alone."""
+    settings = {"d_model": 32, "num_layers": 1, "n_heads": 4, "kv_heads": 2, "value_bins": 8}
+    state = {name: value.double() if value.is_floating_point() else value for name, value in small_state(settings).state_dict().items()}
+    for name in ("Q.weight", "Q.bias", "K.weight", "K.bias", "template_mix.weight", "template_mix.bias", "mlp.down_projection.weight",
+                 "input_scale"):
+        state[f"encoder.0.{name}"] = torch.zeros_like(state[f"encoder.0.{name}"])
+    state["encoder.0.residual_scale"] = torch.ones(1, dtype=torch.float64)
+    boards = random_boards(3, seed=9)
+    embedded = network._embedding(state, boards, torch.float64)
+    rms = lambda x, gain: x / torch.sqrt((x * x).mean(-1, keepdim=True) + 1e-5) * gain
+    values = rms(embedded, state["encoder.0.ln1.weight"]) @ state["encoder.0.V.weight"].T + state["encoder.0.V.bias"]     # B x 70 x 16
+    per_head = values.reshape(3, 70, 2, 8).mean(1).repeat_interleave(2, 1).reshape(3, 1, 32)          # each head reads its group's mean
+    x = embedded + per_head @ state["encoder.0.combine_heads.weight"].T + state["encoder.0.combine_heads.bias"]
+    expected = network._heads(state, rms(x, state["ln.weight"]), settings)
+    found = network.fp32_forward(state, settings, boards, dtype=torch.float64)
+    assert all(torch.allclose(a.double(), b, atol=1e-5) for a, b in zip(found, expected))
+
+
+def test_the_heads_with_identity_projections_are_dot_products_of_squares():
+    """The oracle's heads with the from and to projections the identity (biases zero) and the promotion projection a known
+    constant: a move's logit is x[from] . x[to] / sqrt(d), plus that constant's piece column on a promotion; a1b1 (id 0)
+    and a7a8n (id 1792, knight column) checked by hand."""
+    settings = {"d_model": 32, "num_layers": 1, "n_heads": 4, "value_bins": 8}
+    state = {name: value.double() if value.is_floating_point() else value for name, value in small_state(settings).state_dict().items()}
+    for side in ("from", "to"):
+        state[f"{side}_projection.weight"], state[f"{side}_projection.bias"] = torch.eye(32, dtype=torch.float64), torch.zeros(32, dtype=torch.float64)
+    state["promotion_projection.weight"] = torch.zeros(4, 32, dtype=torch.float64)
+    state["promotion_projection.bias"] = torch.tensor([1.0, 2.0, 3.0, 4.0], dtype=torch.float64)
+    x = torch.randn(2, 70, 32, dtype=torch.float64)
+    logits, _ = network._heads(state, x, settings)
+    assert torch.allclose(logits[:, 0], (x[:, 0] * x[:, 1]).sum(-1) / math.sqrt(32))
+    assert torch.allclose(logits[:, 1792], (x[:, 48] * x[:, 56]).sum(-1) / math.sqrt(32) + 1.0)
 
 
 def test_the_oracles_forward_is_the_models():
