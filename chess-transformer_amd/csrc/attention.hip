@@ -1,12 +1,10 @@
 // Fused template attention over one position's T tokens (64 squares, then T - 64 metadata tokens).
 // Computes what model/fused_blocks.py:35-97 (template_bias_kernel + template_attention_kernel) and
-// model/attention_cuda.py:97-304 compute, for any head counts and widths, in this order (which differs from the
-// reference's only in where fp16 roundings fall, and is held to its tolerance):
-//   q' = f16((q * rsqrt(mean(q^2) + eps)) * (q_gain * k_gain))     the key gain moved to the query side
-//   r_j = rsqrt(mean(k_j^2) + eps)                                  one scale a raw key; keys are never normalised
-//   s[i, j] = (q'_i . k_j) * r_j * scale + [i, j < 64] f16(sum_t c[b, i, h, t] templates[t, i, j])
+// model/attention_cuda.py:97-304 compute, for any head counts and widths, with the reference's fp16 rounding points:
+//   q' = f16((q * (1 / sqrt(mean(q^2) + eps))) * q_gain),  k' = f16((k * (1 / sqrt(mean(k^2) + eps))) * k_gain)
+//   s[i, j] = (q'_i . k'_j) * scale + [i, j < 64] f16(sum_t c[b, i, h, t] templates[t, i, j])
 //   out_i = sum_j f16(exp(s_ij - max_i)) v_j / sum_j exp(s_ij - max_i)
-// (the reference rounds the normalised keys to fp16 and multiplies by the gains on the key side).
+// in f32 (MFMA products of the fp16 operands are exact; sums are f32).
 // projected[B, T, H*dq | KV*dq | KV*dv | H*tc] in, out[B, T, H*dv] (fp16). The templates come key-major,
 // keyed[i][j][t] (8 templates a key, zero past templates_count), so that a lane reads its query's
 // templates for 4 keys as 4 16-byte loads (the reference pairs its templates likewise,
@@ -86,14 +84,13 @@ struct Layout {
     static constexpr int KEYS = TILES * 16;           // keys (and queries) staged
     static constexpr int VKEYS = STEPS * 32;          // value keys staged (P is zero past T)
     static constexpr int KC = DQP / 8, VC = DV / 8;   // 16-byte chunks a raw key (query) row, a raw value row
-    // LDS in bytes: two buffers of raw keys, two of raw values, the keys' scales, then two buffers of raw queries and
-    // template coefficients
+    // LDS in bytes: two buffers of keys (raw as they land, normalised in place), two of raw values, then two buffers of
+    // raw queries and template coefficients
     static constexpr int RAW_K_BYTES = KEYS * DQP * 2;   // a buffer's
     static constexpr int RAW_V_BYTES = VKEYS * DV * 2;   // a buffer's
-    static constexpr int SCALES_BYTES = KEYS * 4;
     static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
     static constexpr int COEF_BYTES = 64 * MAX_TEMPLATES * 2;   // a head's template coefficients, a square query a row
-    static constexpr int FIXED_BYTES = 2 * RAW_K_BYTES + 2 * RAW_V_BYTES + SCALES_BYTES;
+    static constexpr int FIXED_BYTES = 2 * RAW_K_BYTES + 2 * RAW_V_BYTES;
     static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * (RAW_Q_BYTES + COEF_BYTES); }
 };
 
@@ -154,8 +151,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     extern __shared__ __align__(16) int8_t lds[];
     LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)lds;                        // [2][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_v = raw_k + 2 * L::RAW_K_BYTES;                    // [2][VKEYS * DV halves]
-    float* key_scales = (float*)(lds + 2 * L::RAW_K_BYTES + 2 * L::RAW_V_BYTES);   // [KEYS]: the scale times the key's rsqrt
-    LDS_SPACE int8_t* raw_q = raw_v + 2 * L::RAW_V_BYTES + L::SCALES_BYTES;  // [2][per_kv][KEYS * DQP halves]
+    LDS_SPACE int8_t* raw_q = raw_v + 2 * L::RAW_V_BYTES;                    // [2][per_kv][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -215,25 +211,30 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             if (template_query >= 64) templates[kt][j] = uint4{0, 0, 0, 0};
         }
 
-    // The keys are not normalised in place: the scores are s = scale rsqrt_k sum_d (q_n[d] k_gain[d]) k[d], the query
-    // side taking both gains (f32 q_gain k_gain, zero past dq) and rounding to f16 once, the key side its raw f16 row
-    // and a per-key scale.
+    // The query gains of this lane's query columns (zero past dq), and the key gains of this thread's key columns: the keys
+    // are normalised in LDS by four adjacent threads a key, KC / 4 chunks each.
     float gains[DQP / 32][8];
 #pragma unroll
     for (int ks = 0; ks < DQP / 32; ks++)
 #pragma unroll
         for (int e = 0; e < 8; e++) {
             const int d = ks * 32 + quad * 8 + e;
-            const float gain = (float)q_gain[min(d, dq - 1)] * (float)k_gain[min(d, dq - 1)];
-            gains[ks][e] = d < dq ? gain : 0.0f;
+            gains[ks][e] = d < dq ? (float)q_gain[min(d, dq - 1)] : 0.0f;
         }
-    // the key scales: four adjacent threads a key, KC / 4 chunks each
     constexpr int PART_CHUNKS = KC / 4;
     static_assert(KEYS * 4 == THREADS && KC % 4 == 0, "four threads a key");
     const int scale_key = tid / 4, first_chunk = (tid % 4) * PART_CHUNKS;
+    float key_gains[PART_CHUNKS][8];
+#pragma unroll
+    for (int c = 0; c < PART_CHUNKS; c++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int d = (first_chunk + c) * 8 + e;
+            key_gains[c][e] = d < dq ? (float)k_gain[min(d, dq - 1)] : 0.0f;
+        }
     // the staged outputs this thread writes out: row item / VC, chunk item % VC of each head
     constexpr int O_TOTAL = KEYS * VC, O_ITEMS = (O_TOTAL + THREADS - 1) / THREADS;
-    const float inverse_dq = 1.0f / (float)dq;
+    const float columns = (float)dq;
     // The templates and gains have landed before the loop (with the first group's rows): counting loads across the
     // loop's iterations, the compiler would otherwise wait for every load in flight -- the next group's rows too --
     // at each use of them in the loop.
@@ -273,26 +274,31 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
         if (gi + 1 < groups_per_block) dma_group(pair + 1, buffer ^ 1, true, false);
         if (STAGED && gi > 0) write_out(pair - 1, buffer ^ 1);
 
-        // the keys' scales: scale * rsqrt(mean of squares + eps) over the key's dq columns. Past dq a raw key chunk
-        // holds another head's columns: zeroed here, as a zero query column would not cancel an infinite one.
+        // the keys normalised in place: k' = f16((k * (1 / sqrt(mean of squares + eps))) * k_gain) over the key's dq columns,
+        // the four threads of a key adding their partial sums as (a + b) + (c + d). Past dq a raw key chunk holds another
+        // head's columns: zeroed, as a zero query column would not cancel an infinite one.
         {
             LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
+            v8h raw[PART_CHUNKS];
             float squares = 0.0f;
 #pragma unroll
             for (int c = 0; c < PART_CHUNKS; c++) {
-                LDS_SPACE int8_t* chunk = keys + raw_slot<KC>(scale_key, first_chunk + c) * 16;
-                v8h raw = *reinterpret_cast<const LDS_SPACE v8h*>(chunk);
-                if ((first_chunk + c) * 8 >= dq) {
-                    raw = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-                    *reinterpret_cast<LDS_SPACE v8h*>(chunk) = raw;
-                }
-                squares = squares8(raw, squares);
+                raw[c] = *reinterpret_cast<const LDS_SPACE v8h*>(keys + raw_slot<KC>(scale_key, first_chunk + c) * 16);
+                if ((first_chunk + c) * 8 >= dq) raw[c] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+                squares = squares8(raw[c], squares);
             }
             squares += lane_xor1(squares);
             squares += lane_xor2(squares);
-            if (tid % 4 == 0) key_scales[scale_key] = __builtin_amdgcn_rsqf(squares * inverse_dq + eps) * scale;
+            const float inverse = 1.0f / __builtin_sqrtf(squares / columns + eps);
+#pragma unroll
+            for (int c = 0; c < PART_CHUNKS; c++) {
+                v8h normed;
+#pragma unroll
+                for (int e = 0; e < 8; e++) normed[e] = (half_t)(((float)raw[c][e] * inverse) * key_gains[c][e]);
+                *reinterpret_cast<LDS_SPACE v8h*>(keys + raw_slot<KC>(scale_key, first_chunk + c) * 16) = normed;
+            }
         }
-        lds_barrier();   // the keys' scales (and zeroed chunks) are in place, and every wavefront's outputs are read
+        lds_barrier();   // the normalised keys are in place, and every wavefront's outputs are read
         if (gi + 1 < groups_per_block) dma_group(pair + 1, buffer ^ 1, false, true);
 
         for (int hi = 0; hi < per_kv; hi++) {
@@ -330,7 +336,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             }
             squares += __shfl_xor(squares, 16, 64);
             squares += __shfl_xor(squares, 32, 64);
-            const float q_inverse = __builtin_amdgcn_rsqf(squares * inverse_dq + eps);
+            const float q_inverse = 1.0f / __builtin_sqrtf(squares / columns + eps);
             v8h qf[DQP / 32];
 #pragma unroll
             for (int ks = 0; ks < DQP / 32; ks++)
@@ -362,7 +368,6 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                     const v8h kf = *reinterpret_cast<const LDS_SPACE v8h*>(keys + raw_slot<KC>(kt * 16 + col, ks * 4 + quad) * 16);
                     acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf[ks], acc, 0, 0, 0);
                 }
-                const v4f key_scale = *reinterpret_cast<const v4f*>(key_scales + kt * 16 + quad * 4);
                 v4f bias = v4f{0, 0, 0, 0};
                 if (kt < 4) {
 #pragma unroll
@@ -371,7 +376,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                 }
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
-                    float value = acc[r] * key_scale[r];
+                    float value = acc[r] * scale;
                     if (kt < 4) {
                         value += (float)(half_t)bias[r];
                     } else if (kt * 16 + quad * 4 + r >= T) {

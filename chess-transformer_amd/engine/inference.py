@@ -1,13 +1,17 @@
-"""The networks the engine evaluates and the CUDA-graph lanes that serve them, as the reference's engine/inference.py
-builds them: answer_rows, FP16_RESIDUAL_SCALE, fp16_model and int8_model (:19-23, 238-278), and the graph lanes with
-their lean answer rows (Lane, GraphedBatches, ImmediateBatches, serve and the graph sizes, :25-235). A lean lane's
-answers are gathered on the GPU by chess_lean_answers, straight from the move logits and the expected scores, and its
-launch and collect call the HIP runtime by address through engine.hip_runtime, as the native round loop does.
+"""The networks the engine evaluates and the graph lanes that run them: the module API of the reference's
+engine/inference.py (answer_rows, FP16_RESIDUAL_SCALE, fp16_model, int8_model, cpu_batches, GraphedBatches, Lane,
+ImmediateBatches, small_graph_sizes, graph_sizes, chunk_positions), over this build's HIP kernels.
+
+A lane owns a stream, pinned host buffers and one HIP graph per batch size, recorded into a memory pool of its own; a
+batch launches into the smallest graph that holds it on a free lane and is collected later, in any order. A lean lane
+reads board rows that carry the legal moves' answer columns (the native round loop's format) and answers only those
+columns, gathered on the GPU from the answer rows the heads write; its launch and collect go through the HIP runtime's
+entry points by address (engine.hip_runtime), which is how the native loop drives it too. The names of a lane's raw
+handles are the ones that loop reads.
 """
 from __future__ import annotations
 
 from collections.abc import Callable
-from multiprocessing import connection
 from pathlib import Path
 
 import numpy as np
@@ -20,53 +24,54 @@ from model.encoding import NUM_MOVE_IDS, START_POSITION_TOKENS, TOKENS_PER_BOARD
 from model.hip_kernels import check, library_for, pointer, stream_of
 from model.model import expected_score
 
-#scales the residual stream down so its channels stay below fp16's largest number, 65,504
+# the fp16 network's residual stream is scaled by this, so that its channels stay below fp16's largest number, 65,504
 FP16_RESIDUAL_SCALE = 1 / 16
+# a board's answer: its move logits, then its expected score (reference engine/selfplay.py:46)
+ANSWER_WIDTH = NUM_MOVE_IDS + 1
+# a lean board row: the tokens, then LEAN_COLUMNS little-endian int16 indices into the answer row -- the legal moves' logits
+# in the search's order, padded with the expected score's index (the native crate's constants, reference
+# engine/selfplay_rs/src/lib.rs:330-333)
+LEGAL_SLOTS = 218
+LEAN_COLUMNS = LEGAL_SLOTS + 1
+LEAN_ROW = TOKENS_PER_BOARD + 2 * LEAN_COLUMNS
 
 
-#a row per board: the move logits, then the expected score
 def answer_rows(outputs: tuple[torch.Tensor, torch.Tensor] | torch.Tensor) -> torch.Tensor:
+    """B x ANSWER_WIDTH f32 from a network's outputs: the rows themselves, or the move logits and the value logits' expected score."""
     if isinstance(outputs, torch.Tensor):
         return outputs
-    move_logits, value_logits = outputs
-    return torch.cat([move_logits.float(), expected_score(value_logits).unsqueeze(1)], dim=1)
+    logits, value_logits = outputs
+    rows = torch.empty(logits.shape[0], logits.shape[1] + 1, device=logits.device, dtype=torch.float32)
+    rows[:, :-1] = logits
+    rows[:, -1] = expected_score(value_logits)
+    return rows
 
 
 def fused_model(model: nn.Module) -> nn.Module:
-    """An fp32 ChessTransformer (on the GPU) as the fp16 inference network: residual stream scaled by 1/16, all but the heads in fp16."""
+    """An fp32 ChessTransformer as the fp16 inference network: the residual stream scaled by FP16_RESIDUAL_SCALE, everything but
+    the heads in fp16."""
     from model.fused_blocks import FusedTransformer
     return FusedTransformer(model.scale_residual_stream(FP16_RESIDUAL_SCALE).half_except_heads(torch.float16))
 
 
 def fp16_model(checkpoint_path: Path) -> nn.Module:
-    """The network in fp16 (f32 sums), the heads in fp32."""
+    """The checkpoint's network in fp16 on the GPU (f32 sums), the heads in f32."""
     return fused_model(load_model(checkpoint_path, torch.device("cuda")))
 
 
 def int8_model(checkpoint_path: Path, fp16_blocks: int, weights: dict | None = None) -> nn.Module:
-    """fp16_model with every block in int8 but the last and the fp16_blocks whose int8 costs the policy most.
-    weights: the rounded weights (engine/quantization.py) if already read, else rounded once per checkpoint."""
-    from model.int8_blocks import quantize_blocks
+    """fp16_model with every block in int8 but the last and the fp16_blocks whose rounding moves the policy most; weights: the
+    rounded weights (engine/quantization.py) when already read, else read from the cache or computed once."""
     from engine.quantization import int8_weights
-    if weights is None:
-        weights = int8_weights(checkpoint_path, fp16_blocks)
-    return quantize_blocks(fp16_model(checkpoint_path), weights, FP16_RESIDUAL_SCALE)
+    from model.int8_blocks import quantize_blocks
+    rounded = int8_weights(checkpoint_path, fp16_blocks) if weights is None else weights
+    return quantize_blocks(fp16_model(checkpoint_path), rounded, FP16_RESIDUAL_SCALE)
 
 
 def int8_network(model: nn.Module, weights: dict) -> nn.Module:
-    """int8_model for a model already in memory (fp32, on the GPU): the benchmark's and the tests' random-init networks."""
+    """int8_model of a model already in memory (fp32, on the GPU): the tests' and the benchmark's random-init networks."""
     from model.int8_blocks import quantize_blocks
     return quantize_blocks(fused_model(model), weights, FP16_RESIDUAL_SCALE)
-
-
-#answers a board: the move logits, then the expected score (reference engine/selfplay.py:46)
-ANSWER_WIDTH = NUM_MOVE_IDS + 1
-#a lean answer is the legal moves' logits in the search's order, padded with the expected score's index to
-#LEGAL_SLOTS + 1 columns; a lean board row is the board's tokens, then those columns' int16 indices (the native crate's
-#constants, reference engine/selfplay_rs/src/lib.rs:330-333, imported there from selfplay_rs)
-LEGAL_SLOTS = 218
-LEAN_COLUMNS = LEGAL_SLOTS + 1
-LEAN_ROW = TOKENS_PER_BOARD + 2 * LEAN_COLUMNS
 
 
 @torch.library.custom_op("chess::lean_answers", mutates_args=())
@@ -91,81 +96,70 @@ def _(answers, rows, columns_at, columns):
     return answers.new_empty(answers.shape[0], columns)
 
 
-#a lean lane's answers for boards whose rows (tokens, then LEAN_COLUMNS int16 indices) are rows
 def lean_rows(outputs: tuple[torch.Tensor, torch.Tensor] | torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """A lean lane's answers: the LEAN_COLUMNS columns that each board row names."""
     return lean_answers(answer_rows(outputs), rows, TOKENS_PER_BOARD, LEAN_COLUMNS)
 
 
-#the L2 a position's activations take between a block's kernels, per unit of the model's width (reference :25-32)
+# the L2 bytes a position's activations take between a block's kernels, per unit of the model's width; a forward takes at
+# most as many positions as the lanes in flight leave room for in the L2 (reference :25-32)
 L2_BYTES_PER_POSITION_WIDTH = 1024
 MIN_CHUNK_POSITIONS = 64
 
 
 def chunk_positions(width: int, lanes: int) -> int:
+    """Positions a forward: the L2's share a lane, in positions of this width, down to a multiple of 16, at least 64."""
     l2_bytes = torch.cuda.get_device_properties(torch.cuda.current_device()).L2_cache_size
-    return max(MIN_CHUNK_POSITIONS, l2_bytes // (lanes * width * L2_BYTES_PER_POSITION_WIDTH) // 16 * 16)
+    fitting = l2_bytes // (lanes * width * L2_BYTES_PER_POSITION_WIDTH)
+    return max(MIN_CHUNK_POSITIONS, fitting - fitting % 16)
 
 
 def chunked_answer_rows(model: nn.Module, boards: torch.Tensor, chunk: int | None) -> torch.Tensor:
-    parts = [answer_rows(model(part)) for part in boards.split(chunk or len(boards))]
-    return parts[0] if len(parts) == 1 else torch.cat(parts)
+    rows = [answer_rows(model(part)) for part in boards.split(chunk or len(boards))]
+    return torch.cat(rows) if len(rows) > 1 else rows[0]
 
 
 def chunked_lean_rows(model: nn.Module, boards: torch.Tensor, rows: torch.Tensor, chunk: int | None) -> torch.Tensor:
     step = chunk or len(boards)
-    parts = [lean_rows(model(part), part_rows) for part, part_rows in zip(boards.split(step), rows.split(step))]
-    return parts[0] if len(parts) == 1 else torch.cat(parts)
+    answers = [lean_rows(model(part), part_rows) for part, part_rows in zip(boards.split(step), rows.split(step))]
+    return torch.cat(answers) if len(answers) > 1 else answers[0]
 
 
-def serve(network, boards: list[np.ndarray], answers: list[np.ndarray], connections: list, stop, served_calls, served_positions) -> None:
-    """Answers the searches' requests (a count of boards in the slot's shared array) in batches, one batch on the GPU while
-    the next gathers (reference :36-59)."""
-    slot_of = {id(end): slot for slot, end in enumerate(connections)}
-
-    def hand_out(requests: list[tuple[int, int]], launched) -> None:
-        evaluated = network.collect(launched)
-        offset = 0
-        for slot, count in requests:
-            answers[slot][:count] = evaluated[offset:offset + count]
-            offset += count
-            connections[slot].send(True)
-        served_calls.value += 1
-        served_positions.value += offset
-
-    in_flight = None
-    while not stop.is_set():
-        #with a batch on the GPU, take only the requests already waiting, so that its answers wait for nothing more
-        ready = connection.wait(connections, timeout=0 if in_flight else 0.1)
-        requests = [(slot_of[id(end)], end.recv()) for end in ready]
-        started = (requests, network.launch(np.concatenate([boards[slot][:count] for slot, count in requests]))) if requests else None
-        if in_flight is not None:
-            hand_out(*in_flight)
-        in_flight = started
+def _ladder(top: int) -> list[int]:
+    """1, 2, 4, 8, 16, then each size a sixteenth larger (by 4 at least), to top: a batch pads by under a sixteenth past 16."""
+    sizes = [1]
+    while sizes[-1] < top:
+        size = sizes[-1]
+        sizes.append(min(top, 2 * size if size < 16 else size + max(4, size // 16)))
+    return sizes
 
 
 def small_graph_sizes(max_batch: int, chunk: int | None = None) -> list[int]:
-    """Graph sizes 1 to max_batch: doubling to 16, then steps of a sixteenth (at least 4); past a chunk, whole chunks plus
-    the same steps, so that no batch pads into a forward of its own (reference :61-69)."""
-    chunk = min(chunk or max_batch, max_batch)
-    steps = [1]
-    while steps[-1] < chunk:
-        steps.append(min(chunk, steps[-1] * 2 if steps[-1] < 16 else steps[-1] + max(4, steps[-1] // 16)))
-    sizes = [whole + step for whole in range(0, max_batch, chunk) for step in steps]
-    last = next(index for index, size in enumerate(sizes) if size >= max_batch)
-    return sizes[:last + 1]
+    """Graph sizes from 1 to max_batch for the small-batch engine: the ladder within a chunk, then whole chunks plus the
+    ladder, so that no batch pads into a forward of its own (reference :61-69); up to the first size that holds max_batch."""
+    every = min(chunk or max_batch, max_batch)
+    sizes = []
+    for whole in range(0, max_batch, every):
+        for step in _ladder(every):
+            sizes.append(whole + step)
+            if sizes[-1] >= max_batch:
+                return sizes
+    return sizes
 
 
 def graph_sizes(max_batch: int) -> list[int]:
-    """64, then steps of 64 to 1024, of 128 to 2048 and of 256 past it, until max_batch is held (reference :71-75)."""
+    """Graph sizes for large batches: 64, then steps of 64 below 1,024, of 128 below 2,048 and of 256 after, up to the first
+    that holds max_batch (reference :71-75)."""
     sizes = [64]
     while sizes[-1] < max_batch:
-        sizes.append(sizes[-1] + (64 if sizes[-1] < 1024 else 128 if sizes[-1] < 2048 else 256))
+        size = sizes[-1]
+        sizes.append(size + 64 * (1 if size < 1024 else 2 if size < 2048 else 4))
     return sizes
 
 
 def clear_blas_workspaces() -> None:
-    """Drops the BLAS library's workspaces, so that none made while a graph records lands in that graph's pool (reference
-    :77-82); the heads' small layers run on it."""
+    """Drops the BLAS library's cached workspaces, so that none made while a graph records lands in that graph's pool
+    (reference :77-82). Nothing on this build's path calls BLAS, but a caller's model may."""
     clear = getattr(torch._C, "_cuda_clearCublasWorkspaces", None)
     if clear is not None:
         clear()
@@ -175,125 +169,133 @@ clear_cublas_workspaces = clear_blas_workspaces
 
 
 class Lane:
-    """One batch in flight: a stream, a graph per size in a pool of its own, and the pinned buffers its boards and answers
-    cross in (reference :84-143). A lean lane takes rows of LEAN_ROW bytes (tokens, then LEAN_COLUMNS int16 indices of
-    the answer columns) and answers LEAN_COLUMNS floats a board. warm_up: the model runs once a size before recording."""
+    """One batch in flight at a time: a stream, pinned host buffers, and a graph per size recorded in a pool of its own
+    (lanes sharing a pool would write over each other's activations). A lean lane's boards come as LEAN_ROW-byte rows
+    (rows_array, filled by the caller) and its answers are LEAN_COLUMNS floats a board. warm_up runs the model once per
+    size before recording (a network's later lanes skip it)."""
 
     def __init__(self, model: nn.Module, sizes: list[int], chunk: int | None, lean: bool = False, warm_up: bool = True):
-        self.stream = torch.cuda.Stream()
+        self.lean, self.chunk = lean, chunk
         self.device = torch.cuda.current_device()
-        #launched and not yet collected: another launch would write over its answers
+        self.stream = torch.cuda.Stream()
+        self.done = torch.cuda.Event(blocking=True)
+        # launched and not collected yet: another launch would overwrite its answers
         self.pending = False
-        self.lean = lean
-        largest = sizes[-1]
-        #recorded on a real position
-        self.boards = torch.tensor([START_POSITION_TOKENS], dtype=torch.long, device="cuda").repeat(largest, 1)
-        if lean:
-            self.rows = torch.zeros(largest, LEAN_ROW, dtype=torch.uint8, device="cuda")
+        self._buffers(sizes[-1])
+        self._record(model, sizes, warm_up)
+
+    def _buffers(self, largest: int) -> None:
+        # the graphs record on a real position, the start position's tokens in every row
+        self.boards = torch.tensor(START_POSITION_TOKENS, dtype=torch.long, device="cuda").expand(largest, -1).contiguous()
+        width = LEAN_COLUMNS if self.lean else ANSWER_WIDTH
+        self.answers_host = torch.zeros(largest, width, dtype=torch.float32, pin_memory=True)
+        self.answers_array = self.answers_host.numpy()
+        if self.lean:
+            self.rows = torch.empty(largest, LEAN_ROW, dtype=torch.uint8, device="cuda")
             self.rows[:, :TOKENS_PER_BOARD] = self.boards
-            #every column the expected score's until a launch fills the rows
+            # every column the expected score's until a launch brings real rows
             self.rows[:, TOKENS_PER_BOARD:].view(torch.int16).fill_(ANSWER_WIDTH - 1)
             self.rows_host = torch.zeros(largest, LEAN_ROW, dtype=torch.uint8, pin_memory=True)
             self.rows_array = self.rows_host.numpy()
         else:
             self.boards_host = torch.zeros(largest, TOKENS_PER_BOARD, dtype=torch.long, pin_memory=True)
             self.boards_array = self.boards_host.numpy()
-        self.answers_host = torch.zeros(largest, LEAN_COLUMNS if lean else ANSWER_WIDTH, dtype=torch.float32, pin_memory=True)
-        self.answers_array = self.answers_host.numpy()
-        self.done = torch.cuda.Event(blocking=True)
 
-        #a graph records after warm-up calls off the default stream
-        self.stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(self.stream), torch.no_grad():
-            for size in sizes if warm_up else []:
-                self.answer(model, size, chunk)
-        torch.cuda.current_stream().wait_stream(self.stream)
-
-        #a pool a lane, so that two lanes' graphs never share activations
-        self.pool = torch.cuda.graph_pool_handle()
-        self.graphs, self.answers = {}, {}
-        for size in reversed(sizes):
-            self.graphs[size] = torch.cuda.CUDAGraph()
-            clear_blas_workspaces()
-            with torch.cuda.graph(self.graphs[size], pool=self.pool, stream=self.stream), torch.no_grad():
-                self.answers[size] = self.answer(model, size, chunk)
-            clear_blas_workspaces()
-        #the event has a handle from its first record on
-        self.done.record(self.stream)
-        self.done.synchronize()
-        #a lean collect copies the answers' bytes as they are
-        assert not lean or all(answers.dtype == torch.float32 and answers.is_contiguous() for answers in self.answers.values())
-
-    def answer(self, model: nn.Module, size: int, chunk: int | None) -> torch.Tensor:
+    def answer(self, model: nn.Module, size: int, chunk: int | None = None) -> torch.Tensor:
+        """The forward a graph records: the first size boards (a lean lane's taken from its rows) to answers."""
+        chunk = self.chunk if chunk is None else chunk
         if not self.lean:
             return chunked_answer_rows(model, self.boards[:size], chunk)
         self.boards[:size].copy_(self.rows[:size, :TOKENS_PER_BOARD])
         return chunked_lean_rows(model, self.boards[:size], self.rows[:size], chunk)
 
+    def _record(self, model: nn.Module, sizes: list[int], warm_up: bool) -> None:
+        # graphs record after warm-up calls made off the default stream
+        self.stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(self.stream), torch.no_grad():
+            for size in sizes if warm_up else ():
+                self.answer(model, size)
+        torch.cuda.current_stream().wait_stream(self.stream)
+        self.pool = torch.cuda.graph_pool_handle()
+        self.graphs, self.answers = {}, {}
+        for size in sorted(sizes, reverse=True):      # the largest first: it sizes the pool the smaller ones reuse
+            graph = torch.cuda.CUDAGraph()
+            clear_blas_workspaces()
+            with torch.cuda.graph(graph, pool=self.pool, stream=self.stream), torch.no_grad():
+                self.answers[size] = self.answer(model, size)
+            clear_blas_workspaces()
+            self.graphs[size] = graph
+        # the event gets its handle at its first record
+        self.done.record(self.stream)
+        self.done.synchronize()
+        if self.lean and not all(answers.dtype == torch.float32 and answers.is_contiguous() for answers in self.answers.values()):
+            raise RuntimeError("a lean lane's collect copies its answers' bytes: they must be contiguous f32")
+
     def handles(self) -> dict:
-        """The raw handles a lean launch and collect pass to the HIP runtime; graphs maps a size to (its executable graph, its
-        answers on the device)."""
-        return {"device": self.device, "stream": self.stream.cuda_stream, "done": self.done.cuda_event,
-                "rows_host": self.rows_host.data_ptr(), "rows": self.rows.data_ptr(), "answers_host": self.answers_host.data_ptr(),
+        """The raw handles a lean launch and collect (and the native round loop) pass to the HIP runtime; graphs maps a size to
+        (its executable graph, its answers on the device)."""
+        return {"device": self.device, "stream": self.stream.cuda_stream, "done": self.done.cuda_event, "rows_host": self.rows_host.data_ptr(),
+                "rows": self.rows.data_ptr(), "answers_host": self.answers_host.data_ptr(),
                 "graphs": {size: (graph.raw_cuda_graph_exec(), self.answers[size].data_ptr()) for size, graph in self.graphs.items()}}
 
 
 class GraphedBatches:
-    """The model as graphs in in_flight lanes (reference :145-226): launch returns at once and collect waits, in any
-    order, with at most in_flight batches out. A batch takes the smallest graph that holds it, on the first free lane.
-    chunk: boards a forward (chunk_positions; None: a batch's all at once). blocking_wait: collect sleeps until the batch
-    is done rather than spinning a core. lean: lean lanes, filled by the caller (rows_array) and run by launch_filled."""
+    """The model as graphs on in_flight lanes (reference :145-226): launch returns at once, collect waits; batches may be
+    collected in any order, at most in_flight out at a time. A batch takes the smallest graph that holds it on the first
+    free lane. chunk: boards a forward (chunk_positions; None, a batch's all at once). blocking_wait: collect sleeps on
+    an event rather than spinning a core. lean: lean lanes, filled by the caller (rows_array) and run by launch_filled."""
 
-    def __init__(self, model: nn.Module, sizes: list[int], in_flight: int = 2, chunk: int | None = None,
-                 blocking_wait: bool = False, lean: bool = False):
-        #kept alive: the graphs read its weights where they were recorded
-        self.model = model
-        self.sizes = sizes
-        self.lanes = [Lane(model, sizes, chunk, lean, warm_up=number == 0) for number in range(in_flight)]
-        self.lean = lean
-        self.blocking_wait = blocking_wait
+    def __init__(self, model: nn.Module, sizes: list[int], in_flight: int = 2, chunk: int | None = None, blocking_wait: bool = False,
+                 lean: bool = False):
+        self.model = model        # the graphs read its weights where they were recorded: kept alive with them
+        self.sizes = sorted(sizes)
+        self.lean, self.blocking_wait = lean, blocking_wait
+        self.lanes = [Lane(model, self.sizes, chunk, lean, warm_up=index == 0) for index in range(in_flight)]
         self.runtime = hip_runtime() if lean else None
         self.handles = {id(lane): lane.handles() for lane in self.lanes} if lean else {}
 
+    def free_lane(self) -> Lane:
+        """The lane the next launch takes; the caller may fill its boards_array (a lean lane's rows_array) for launch_filled."""
+        for lane in self.lanes:
+            if not lane.pending:
+                return lane
+        raise RuntimeError("more batches in flight than lanes")
+
+    def _size_for(self, count: int) -> int:
+        for size in self.sizes:
+            if size >= count:
+                return size
+        raise ValueError(f"{count} boards are more than the largest graph's {self.sizes[-1]}")
+
     def launch(self, boards: np.ndarray) -> tuple[Lane, int, int]:
         if self.lean:
-            raise RuntimeError("lean lanes answer rows with their columns (launch_filled), not boards")
+            raise RuntimeError("lean lanes take board rows with their answer columns (launch_filled), not boards")
         lane = self.free_lane()
-        lane.boards_host[:len(boards)] = torch.from_numpy(boards)
+        lane.boards_array[:len(boards)] = boards
         return self.launch_filled(lane, len(boards))
 
-    def free_lane(self) -> Lane:
-        """The lane the next launch takes; a caller may fill its boards_array (a lean lane's rows_array) for launch_filled."""
-        lane = next((lane for lane in self.lanes if not lane.pending), None)
-        if lane is None:
-            raise RuntimeError("more batches in flight than lanes")
-        return lane
-
     def launch_filled(self, lane: Lane, count: int) -> tuple[Lane, int, int]:
-        """Starts the lane's first count boards; a lean lane's calls leave the thread's current device at the lane's."""
-        size = next((size for size in self.sizes if size >= count), None)
-        if size is None:
-            raise ValueError(f"{count} boards are more than the largest graph's {self.sizes[-1]}")
+        """Starts the lane's first count boards. A lean lane's runtime calls leave the thread's current device at the lane's."""
+        size = self._size_for(count)
+        lane.pending = True
         if lane.lean:
             runtime, handles = self.runtime, self.handles[id(lane)]
             stream = handles["stream"]
             runtime.check(runtime.set_device(handles["device"]), "the lane's device")
             runtime.check(runtime.memcpy(handles["rows"], handles["rows_host"], count * LEAN_ROW, HOST_TO_DEVICE, stream), "the boards' copy")
-            lane.pending = True
             runtime.check(runtime.graph_launch(handles["graphs"][size][0], stream), "the graph's launch")
             runtime.check(runtime.event_record(handles["done"], stream), "the batch's event")
-            return lane, size, count
-        lane.pending = True
-        with torch.cuda.stream(lane.stream):
-            lane.boards[:count].copy_(lane.boards_host[:count], non_blocking=True)
-            lane.graphs[size].replay()
-            if self.blocking_wait:
-                lane.done.record(lane.stream)
+        else:
+            with torch.cuda.stream(lane.stream):
+                lane.boards[:count].copy_(lane.boards_host[:count], non_blocking=True)
+                lane.graphs[size].replay()
+                if self.blocking_wait:
+                    lane.done.record(lane.stream)
         return lane, size, count
 
     def collect(self, launched: tuple[Lane, int, int]) -> np.ndarray:
-        """The batch's answers in the lane's pinned buffer. Copied here, not at launch: the GPU's copies queue, so a copy at
-        launch would hold the other lane's boards behind it."""
+        """The batch's answers, in the lane's pinned buffer. They are copied back here rather than at launch: the GPU's copies
+        queue, and one made at launch would hold the other lane's boards behind this batch's forward."""
         lane, size, count = launched
         if lane.lean:
             runtime, handles = self.runtime, self.handles[id(lane)]
@@ -304,14 +306,13 @@ class GraphedBatches:
             answers = handles["graphs"][size][1]
             runtime.check(runtime.memcpy(handles["answers_host"], answers, count * LEAN_COLUMNS * 4, DEVICE_TO_HOST, stream), "the answers' copy")
             runtime.check(runtime.stream_synchronize(stream), "the batch")
-            lane.pending = False
-            return lane.answers_array[:count]
-        if self.blocking_wait:
-            lane.done.synchronize()
-        with torch.cuda.stream(lane.stream):
-            lane.answers_host[:count].copy_(lane.answers[size][:count])
+        else:
+            if self.blocking_wait:
+                lane.done.synchronize()
+            with torch.cuda.stream(lane.stream):
+                lane.answers_host[:count].copy_(lane.answers[size][:count])
         lane.pending = False
-        return lane.answers_host[:count].numpy()
+        return lane.answers_array[:count]
 
     def rust_network(self) -> dict:
         """What the native round loop holds: the lean lanes' handles (it keeps this object, so every lane lives while it runs)."""
@@ -320,6 +321,7 @@ class GraphedBatches:
         return {"blocking_wait": self.blocking_wait, "lanes": [self.handles[id(lane)] for lane in self.lanes]}
 
     def settle(self) -> None:
+        """Waits for every batch in flight and frees its lane, without copying its answers."""
         for lane in self.lanes:
             if lane.pending:
                 lane.stream.synchronize()
@@ -327,7 +329,7 @@ class GraphedBatches:
 
 
 class ImmediateBatches:
-    """GraphedBatches' interface without a GPU: launch does the work (reference :228-235)."""
+    """GraphedBatches' launch and collect without a GPU: launch does the work (reference :228-235)."""
 
     def __init__(self, evaluate_boards: Callable[[np.ndarray], np.ndarray]):
         self.evaluate_boards = evaluate_boards
@@ -337,3 +339,11 @@ class ImmediateBatches:
 
     def collect(self, launched: np.ndarray) -> np.ndarray:
         return launched
+
+
+def cpu_batches(model: nn.Module) -> ImmediateBatches:
+    """The CPU path (reference :274-278): a model on the CPU (the fp32 ChessTransformer) answering batches at launch."""
+    def evaluate_boards(boards: np.ndarray) -> np.ndarray:
+        with torch.no_grad():
+            return answer_rows(model(torch.from_numpy(np.asarray(boards)).long())).numpy()
+    return ImmediateBatches(evaluate_boards)

@@ -436,14 +436,25 @@ def move_places(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 def head_weights(model: ChessTransformer) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The policy head's from x to bilinear form, expanded so that the kernels never form the projections. With W_f, b_f and
+    W_t, b_t the from and to projections and r = sqrt(d):
+        (W_f x_i + b_f) . (W_t x_j + b_t) / r = (x_i A + a) . x_j + x_i . f + c,
+        A = W_f^T W_t / r,  a = W_t^T b_f / r,  f = W_f^T b_t / r,  c = b_f . b_t / r.
+    Returns A (fp16, the `a` matmul's weight, as the reference keeps it: fused_blocks.py:815-823), a (f32), and the narrow
+    projection's rows and biases (f32): [f; the promotion logits; board_down's inputs] and [c; their biases]; all formed
+    in float64 first."""
     with torch.no_grad():
+        root = math.sqrt(model.d_model)
         from_weight, from_bias = model.from_projection.weight.double(), model.from_projection.bias.double()
         to_weight, to_bias = model.to_projection.weight.double(), model.to_projection.bias.double()
         promotion, down = model.promotion_projection, model.board_down_project[0]
-        scale = 1 / math.sqrt(model.d_model)
-        narrow_weight = torch.cat([(to_bias @ from_weight)[None] * scale, promotion.weight.double(), down.weight.double()])
-        narrow_bias = torch.cat([(from_bias @ to_bias)[None] * scale, promotion.bias.double(), down.bias.double()])
-        return ((from_weight.T @ to_weight * scale).half(), (to_weight.T @ from_bias * scale).float(), narrow_weight.float(), narrow_bias.float())
+        pairing = from_weight.t() @ to_weight / root
+        to_side = to_weight.t() @ from_bias / root
+        from_side = from_weight.t() @ to_bias / root
+        constant = torch.dot(from_bias, to_bias) / root
+        narrow = torch.cat([from_side.unsqueeze(0), promotion.weight.double(), down.weight.double()])
+        narrow_bias = torch.cat([constant.reshape(1), promotion.bias.double(), down.bias.double()])
+    return pairing.half(), to_side.float(), narrow.float(), narrow_bias.float()
 
 
 class FusedTransformer(nn.Module):

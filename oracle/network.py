@@ -7,7 +7,9 @@ state_dict (the reference's checkpoint format, model/checkpoint.py:22-23) and ne
   input_embedding      model/fused_blocks.py:370-393 (input_embedding_kernel): the features summed in f32 in slot order
   fp32_forward         model/model.py:71-99, 245-270: the reference's CPU path (engine/inference.py:274-278)
   int8_forward         engine/inference.py:238-272 + model/int8_blocks.py:254-298 + model/fused_blocks.py:325-363:
-                       the fp16 network (stream scaled by 1/16) with int8 blocks from int8_ops, and the fp32 heads
+                       the fp16 network (stream scaled by 1/16) with int8 blocks from int8_ops, and the heads of the
+                       reference's int8 network (int8_path_heads: model/fused_blocks.py:815-823, 863-874, A in fp16)
+  square_feature_rows_fast  the same rows as square_feature_rows with numpy array operations (the CPU baseline's forward)
 
 Parity of fp32_forward is pinned by the reference's own known answers (tests/test_oracle.py): the square-feature
 rows of a known position (reference tests/test_model.py:166-186), grouped-query attention equal to full attention
@@ -165,6 +167,34 @@ def _heads(state: dict, output: torch.Tensor, settings: dict) -> tuple[torch.Ten
     return moves, value
 
 
+def int8_path_heads(state: dict, output: torch.Tensor, settings: dict) -> tuple[torch.Tensor, torch.Tensor]:
+    """The heads of the reference's int8 network (model/fused_blocks.py:863-874, the heads without fused ends, with the
+    weights of head_weights, :815-823), in float64 from the final norm's fp16 rows: the from x to bilinear form expanded as
+    (W_f x + b_f) . (W_t y + b_t) / sqrt(d) = (x A + a_bias) . y + s(x) with A = W_f^T W_t / sqrt(d) rounded to fp16 and
+    a_bias = W_t^T b_f / sqrt(d), s(x) = x . (W_f^T b_t) / sqrt(d) + b_f . b_t / sqrt(d), and the narrow products (s, the
+    promotion logits, board_down's inputs) from f32 weights; then the moves gathered, the promotions added, the value head."""
+    d = output.shape[-1]
+    scale = 1 / math.sqrt(d)
+    w = lambda name: _tensor(state, name)
+    from_weight, from_bias, to_weight, to_bias = w("from_projection.weight"), w("from_projection.bias"), w("to_projection.weight"), w("to_projection.bias")
+    A = (from_weight.T @ to_weight * scale).half().double()
+    a_bias = (to_weight.T @ from_bias * scale).float().double()
+    narrow_weight = torch.cat([(to_bias @ from_weight)[None] * scale, w("promotion_projection.weight"), w("board_down_project.0.weight")]).float().double()
+    narrow_bias = torch.cat([(from_bias @ to_bias)[None] * scale, w("promotion_projection.bias"), w("board_down_project.0.bias")]).float().double()
+    a = output @ A + a_bias
+    narrow = output @ narrow_weight.T + narrow_bias
+    squares = output[:, :NUM_SQUARES]
+    logits = a[:, :NUM_SQUARES] @ squares.transpose(1, 2) + narrow[:, :NUM_SQUARES, :1]
+    from_squares, to_squares = state["from_squares"].cpu(), state["to_squares"].cpu()
+    promotion_ids, promotion_to, promotion_pieces = (state[n].cpu() for n in ("promotion_move_ids", "promotion_to_squares", "promotion_pieces"))
+    moves = logits[:, from_squares, to_squares]
+    promotions = narrow[:, :NUM_SQUARES, 1:1 + w("promotion_projection.weight").shape[0]]
+    moves[:, promotion_ids] += promotions[:, promotion_to, promotion_pieces]
+    compressed = F.gelu(narrow[..., 1 + promotions.shape[-1]:]).reshape(len(output), -1)
+    value = F.gelu(compressed @ w("eval_head.0.weight").T + w("eval_head.0.bias")) @ w("eval_head.2.weight").T + w("eval_head.2.bias")
+    return moves, value
+
+
 def _attention(state: dict, prefix: str, normed: torch.Tensor, templates: torch.Tensor, heads: int, eps: float = EPS) -> torch.Tensor:
     B, T, d = normed.shape
     dtype = normed.dtype
@@ -312,4 +342,4 @@ def int8_forward(state: dict, settings: dict, weights: dict, boards: torch.Tenso
         else:
             x = _fp16_block(half, layer, x, templates, original, heads, input_mixed, next_scales)
     output = _rms(torch.from_numpy(x.astype(np.float64)), half["ln.weight"].double()).half().double()
-    return tuple(t.float() for t in _heads(state, output, settings))
+    return tuple(t.float() for t in int8_path_heads(state, output, settings))

@@ -13,6 +13,7 @@ from engine.inference import (ANSWER_WIDTH, LEAN_COLUMNS, LEAN_ROW, GraphedBatch
                               int8_network, lean_answers, small_graph_sizes)
 from engine.quantization import nearest_int8_weights
 from model.encoding import NUM_MOVE_IDS, START_POSITION_TOKENS, TOKENS_PER_BOARD
+from model.model import expected_score
 
 
 @pytest.mark.parametrize("max_batch, chunk", [(64, None), (300, None), (64, 64), (256, 64), (300, 48)])
@@ -55,6 +56,19 @@ def test_the_start_position_tokens():
     # the reference's START_POSITION_ENCODING (tests/test_board_encoding.py:43-52), its token numbers written out
     expected = [4, 2, 3, 5, 6, 3, 2, 4] + [1] * 8 + [0] * 32 + [7] * 8 + [10, 8, 9, 11, 12, 9, 8, 10] + [14] + [16] * 4 + [17]
     assert list(START_POSITION_TOKENS) == expected and len(expected) == TOKENS_PER_BOARD
+
+
+def test_the_cpu_path_answers_at_launch():
+    """cpu_batches (the reference's CPU path, engine/inference.py:274-278): a CPU model's answer rows, at launch."""
+    from engine.inference import cpu_batches
+    from model.model import ChessTransformer
+    torch.manual_seed(0)
+    model = ChessTransformer(d_model=32, num_layers=1, n_heads=2, value_bins=8).eval()
+    boards = np.array([START_POSITION_TOKENS] * 3)
+    answers = cpu_batches(model).launch(boards)
+    with torch.no_grad():
+        logits, values = model(torch.from_numpy(boards))
+    assert answers.shape == (3, ANSWER_WIDTH) and np.allclose(answers[:, :-1], logits.numpy()) and np.allclose(answers[:, -1], expected_score(values).numpy())
 
 
 def test_immediate_batches_answer_at_launch():
@@ -201,29 +215,3 @@ def test_batches_in_flight_together_answer_as_alone(network):
             lane.rows_array[:256] = batch_rows
             launched.append(lean.launch_filled(lane, 256))
         assert np.array_equal([lean.collect(one).copy() for one in launched], expected)
-
-
-def test_serve_answers_each_slot_its_boards():
-    """serve on the CPU with ImmediateBatches: each search's request (a count of boards in its slot) is answered in its
-    slot's array, and the counters add up (reference engine/inference.py:36-59)."""
-    import threading
-    from multiprocessing import Pipe
-
-    from engine.inference import serve
-
-    pairs = [Pipe() for _ in range(3)]
-    boards = [np.full((4, TOKENS_PER_BOARD), slot, dtype=np.uint8) for slot in range(3)]
-    answers = [np.zeros((4, 1), dtype=np.float32) for _ in range(3)]
-    stop, calls, positions = threading.Event(), SimpleNamespace(value=0), SimpleNamespace(value=0)
-    network = ImmediateBatches(lambda batch: batch[:, :1].astype(np.float32) * 10)
-    server = threading.Thread(target=serve, args=(network, boards, answers, [served for served, _ in pairs], stop, calls, positions))
-    server.start()
-    try:
-        for slot, count in ((0, 2), (2, 4), (1, 1)):
-            pairs[slot][1].send(count)
-            assert pairs[slot][1].poll(10) and pairs[slot][1].recv() is True
-            assert np.array_equal(answers[slot][:count], np.full((count, 1), 10 * slot))
-    finally:
-        stop.set()
-        server.join(10)
-    assert positions.value == 7 and calls.value >= 1

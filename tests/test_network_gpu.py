@@ -147,9 +147,9 @@ def test_the_move_logits_are_the_heads_torch_ops(device, settings):
 
 @pytest.mark.parametrize("settings", [SMALL, FULL])
 def test_the_heads_are_the_oracles(device, settings):
-    """chess::heads from the final norm's rows: the value logits and the expected score against the oracle's heads in float64
-    (the reference's model/model.py:264-268 and expected_score), the move logits against the torch ops of the heads' own
-    formulation (the fp16 `a` of reference fused_blocks.py:815-823), and the answer rows as the forward returns them."""
+    """chess::heads from the final norm's rows against the oracle's heads of the reference's int8 network in float64
+    (oracle/network.py int8_path_heads: reference fused_blocks.py:815-823, 863-874): the move logits, the value logits and
+    the expected score within 1e-4, as the forward's answer rows and value logits."""
     model = make_model(settings, seed=13)
     state = {name: value.clone() for name, value in model.state_dict().items()}
     fused = fused_blocks.FusedTransformer(copy.deepcopy(model).scale_residual_stream(FP16_RESIDUAL_SCALE).half_except_heads(torch.float16)).to(device)
@@ -158,17 +158,12 @@ def test_the_heads_are_the_oracles(device, settings):
     x = torch.randn(B, 70, D).half()
     with torch.no_grad():
         rows, value_logits = fused.answers(x.to(device))
-    moves, values = oracle_network._heads(state, x.double(), settings)
+    moves, values = oracle_network.int8_path_heads(state, x.double(), settings)
     rows, value_logits = rows.cpu().double(), value_logits.cpu().double()
     assert rows.shape == (B, moves.shape[1] + 1) and value_logits.shape == values.shape
+    assert torch.allclose(rows[:, :-1], moves, atol=1e-4, rtol=1e-4)
     assert torch.allclose(value_logits, values, atol=1e-4, rtol=1e-4)
-    assert torch.allclose(rows[:, -1], expected_score(values.double()).double(), atol=1e-4)
-    a = x.double() @ fused.a_weight.cpu().double() + fused.a_bias.cpu().double()
-    narrow = x.double() @ fused.narrow_weight.cpu().double().T + fused.narrow_bias.cpu().double()
-    logits = (a[:, :64] @ x[:, :64].double().transpose(1, 2) + narrow[:, :64, :1])[:, fused.from_squares.cpu(), fused.to_squares.cpu()]
-    logits[:, fused.promotion_move_ids.cpu()] += narrow[:, :64][..., fused.promotion_columns][:, fused.promotion_to_squares.cpu(),
-                                                                                               fused.promotion_pieces.cpu()]
-    assert torch.allclose(rows[:, :-1], logits, atol=1e-4, rtol=1e-4)
+    assert torch.allclose(rows[:, -1], expected_score(values).double(), atol=1e-4)
 
 
 def test_tiles_change_no_answer(device, monkeypatch):

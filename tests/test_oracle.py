@@ -325,6 +325,28 @@ def test_the_heads_with_identity_projections_are_dot_products_of_squares():
     assert torch.allclose(logits[:, 1792], (x[:, 48] * x[:, 56]).sum(-1) / math.sqrt(32) + 1.0)
 
 
+def test_the_int8_paths_heads_are_the_models_where_its_roundings_are_exact():
+    """The heads of the reference's int8 network (A = W_f^T W_t / sqrt(d) in fp16, the bilinear form expanded into a, a_bias
+    and the narrow terms) against the model's heads, with dyadic weights and biases for which A and every f32 weight are
+    exact: then the two are the same function (a dropped term of the expansion, a transposed A or a wrong narrow column
+    fails), up to float64 rounding. With other weights they differ by A's fp16 rounding only."""
+    settings = {"d_model": 16, "num_layers": 1, "n_heads": 2, "value_bins": 8}
+    state = {name: value.double() if value.is_floating_point() else value for name, value in small_state(settings).state_dict().items()}
+    generator = torch.Generator().manual_seed(3)
+    dyadic = lambda *shape: torch.randint(-8, 9, shape, generator=generator).double() / 8
+    state["from_projection.weight"], state["to_projection.weight"] = 2 * torch.eye(16, dtype=torch.float64), torch.diag(dyadic(16)) * 2
+    for name in ("from_projection.bias", "to_projection.bias", "promotion_projection.bias", "board_down_project.0.bias"):
+        state[name] = dyadic(*state[name].shape)
+    for name in ("promotion_projection.weight", "board_down_project.0.weight"):
+        state[name] = dyadic(*state[name].shape)
+    x = torch.randn(3, 70, 16, generator=generator).half().double()
+    for found, expected in zip(network.int8_path_heads(state, x, settings), network._heads(state, x, settings)):
+        assert torch.allclose(found, expected, atol=1e-12)
+    state["from_projection.weight"] = torch.randn(16, 16, generator=generator, dtype=torch.float64)
+    rounded, exact = network.int8_path_heads(state, x, settings)[0], network._heads(state, x, settings)[0]
+    assert 0 < (rounded - exact).abs().max() < 1e-2
+
+
 def test_the_oracles_forward_is_the_models():
     model = small_state(SMALL)
     boards = random_boards(5)
