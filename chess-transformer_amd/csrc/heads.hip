@@ -15,6 +15,8 @@
 // quadrants and the narrow rows meet in LDS for the gather of the 1,968 moves.
 #include "chess_common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int SQUARES = 64;
@@ -264,5 +266,55 @@ extern "C" int chess_value_head(const void* c, const void* hidden_weight, const 
     if (!aligned16(workspace)) return chess_fail(CHESS_MISALIGNED, "value_head reads its workspace 16 bytes a lane");
     if (B == 0) return CHESS_OK;
     return value_head(c, hidden_weight, hidden_bias, out_weight, out_bias, centres, value_logits, rows, (float*)workspace, B, K, H, bins, row_stride,
+                      score_column, (hipStream_t)stream);
+}
+
+// The value head without a workspace argument, for callers that cannot allocate (code under graph capture, serving
+// loops that forbid allocation): the hidden layer goes through `scratch`, a file-scope device array of
+// VALUE_SCRATCH_FLOATS floats (8 MiB: the hidden layer of 4,096 positions at 512 units) that each GPU holds from the
+// library's load until the process ends. Host code reaches the array only through the address hipGetSymbolAddress gives
+// on each device (the array's name in host code is not a device address), looked up once per device, with that
+// device current, on the first call there. Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+// (on two streams, say) race. Every hidden value the second kernel reads was written by the first in the same call,
+// so nothing needs clearing.
+constexpr long long VALUE_SCRATCH_FLOATS = 1LL << 21;
+static __device__ __align__(256) float scratch[VALUE_SCRATCH_FLOATS];
+
+namespace {
+
+constexpr int MAX_DEVICES = 64;
+
+// the scratch array's address on the current device, looked up on the device's first call
+int scratch_address(float** address) {
+    static std::mutex lock;
+    static float* addresses[MAX_DEVICES] = {};
+    int device = 0;
+    if (hipError_t error = hipGetDevice(&device); error != hipSuccess) return (int)error;
+    if (device < 0 || device >= MAX_DEVICES) return chess_fail(CHESS_UNSUPPORTED, "value_head_no_alloc: device %d past the %d it keeps", device, MAX_DEVICES);
+    std::lock_guard<std::mutex> guard(lock);
+    if (!addresses[device]) {
+        void* found = nullptr;
+        if (hipError_t error = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch)); error != hipSuccess) return (int)error;
+        addresses[device] = (float*)found;
+    }
+    *address = addresses[device];
+    return CHESS_OK;
+}
+
+}  // namespace
+
+extern "C" int chess_value_head_no_alloc(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight,
+                                         const void* out_bias, const void* centres, void* value_logits, void* rows, int B, int K, int H, int bins,
+                                         int row_stride, int score_column, void* stream)
+{
+    if (int status = check_value_head(c, hidden_weight, hidden_bias, out_weight, out_bias, centres, rows, B, K, H, bins, row_stride, score_column))
+        return status;
+    if ((long long)B * H > VALUE_SCRATCH_FLOATS)
+        return chess_fail(CHESS_UNSUPPORTED, "value_head_no_alloc holds at most %lld hidden values (%d positions x %d units are %lld)",
+                          VALUE_SCRATCH_FLOATS, B, H, (long long)B * H);
+    if (B == 0) return CHESS_OK;
+    float* hidden = nullptr;
+    if (int status = scratch_address(&hidden)) return status;
+    return value_head(c, hidden_weight, hidden_bias, out_weight, out_bias, centres, value_logits, rows, hidden, B, K, H, bins, row_stride,
                       score_column, (hipStream_t)stream);
 }

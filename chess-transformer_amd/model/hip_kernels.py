@@ -32,6 +32,7 @@ SIGNATURES = {
     "chess_board_embedding": [_pointer, _int] + [_pointer] * 7 + [_int] * 12 + [_pointer],
     "chess_move_logits": [_pointer] * 9 + [_int] * 8 + [_pointer],
     "chess_value_head": [_pointer] * 9 + [ctypes.c_longlong] + [_int] * 6 + [_pointer],
+    "chess_value_head_no_alloc": [_pointer] * 8 + [_int] * 6 + [_pointer],
     "chess_lean_answers": [_pointer] * 3 + [_int] * 5 + [_pointer],
     "chess_runtime_addresses": [ctypes.POINTER(ctypes.c_void_p), _int],
     "chess_error_string": [_int],

@@ -113,6 +113,15 @@ int chess_value_head(const void* c, const void* hidden_weight, const void* hidde
                      const void* centres, void* value_logits, void* rows, void* workspace, long long workspace_bytes, int B, int K, int H,
                      int bins, int row_stride, int score_column, void* stream);
 
+/* chess_value_head without a workspace: the hidden layer goes through the library's own file-scope device array of
+ * 2,097,152 floats (8 MiB a GPU, held from the library's load to the process's end), so that the call allocates
+ * nothing and takes no workspace. B * H above 2,097,152 (4,096 positions at 512 units) is refused (CHESS_UNSUPPORTED).
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race. No counterpart in the reference:
+ * it is for callers that cannot allocate (code under graph capture, serving loops that forbid allocation). */
+int chess_value_head_no_alloc(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias,
+                              const void* centres, void* value_logits, void* rows, int B, int K, int H, int bins, int row_stride,
+                              int score_column, void* stream);
+
 /* The lean lanes' answers (engine/inference.py:131-137, Lane.answer's gather on a lean lane): rows[B][row_bytes] hold at
  * byte columns_at `columns` little-endian int16 indices into a board's answer row (answer_rows[B][width] f32: the moves'
  * logits then the expected score, :19-23; the row layout of engine/selfplay_rs/src/lib.rs:331-333). answers[B][columns]
