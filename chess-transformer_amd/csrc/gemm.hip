@@ -1,5 +1,6 @@
 // The GEMM's C entry points: argument checks, the epilogue's flags, and the dispatch to the translation unit of the
-// operand and output types (gemm_i8_*.hip, gemm_f16.hip; the kernel and its tiles are in gemm_tiles.h).
+// operand and output types (gemm_i8_*.hip, gemm_f16.hip; the kernel and its tiles are in gemm_tiles.h, the split-K tiles for
+// few rows in gemm_split.h).
 #include "gemm.h"
 
 using namespace gemm;

@@ -1,0 +1,272 @@
+// The int8 GEMM for few rows, split over K (what model/int8_cuda.py:34-183, small_int8, does for the reference's one- and
+// two-position batches): out[M, N] = epilogue(x[M, K] @ w[N, K]^T), with gemm_tiles.h's epilogue and op order, so that a
+// split tile gives the whole-K tiles' bits.
+//
+// A workgroup of WAVES wavefronts takes a BM x BN tile of outputs (BM = 32 FM rows, BN = 32 FN columns; gated: BN outputs
+// from the gate's and up's rows). Every wavefront computes the whole tile over its own STEPS x 128 bytes of K, so a tile's
+// sums take 1 / WAVES of the serial K walk of a whole-K tile, and a launch of few rows still has a long queue of loads in
+// flight. The operands go straight from memory to registers, with no LDS ring and no barrier in the main loop: a lane
+// holds 64 contiguous bytes of one row a step (lanes 0-31 a row's first 64 bytes of the step's 128, lanes 32-63 its last
+// 64), so that one load instruction reads whole 128-byte lines. MFMA c of a step takes bytes 16 c .. 16 c + 15 of each
+// lane's 64: which k a byte stands for is the same for both operands, so the sums are the dot products.
+// DEPTH steps of operands are in flight in registers while one is multiplied.
+// The wavefronts' int32 partial tiles meet in LDS ([WAVES][NB][BM][BN + 4]); after one barrier, each thread adds the
+// partials of 8 consecutive columns of a row (int32: exact in any order) and runs the epilogue on them in the row layout,
+// the residual and input embedding read and the outputs written 16 bytes a lane.
+#pragma once
+
+#include "gemm.h"
+#include "lds_dma.h"
+
+#include <type_traits>
+
+namespace split {
+
+using namespace gemm;
+
+typedef int v16i_t __attribute__((ext_vector_type(16)));
+typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+
+constexpr int CHUNK = 128;   // bytes of K a step
+
+template <int FM, int FN, int NB, int WAVES> constexpr int lds_bytes() { return WAVES * NB * 32 * FM * (32 * FN + 4) * 4; }
+
+template <typename OutT> DEVICE void store_eight(OutT* to, const float (&v)[8]);
+template <> DEVICE void store_eight<half_t>(half_t* to, const float (&v)[8]) {
+    const v8h eight = v8h{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+    __builtin_nontemporal_store(eight, reinterpret_cast<v8h*>(to));
+}
+template <> DEVICE void store_eight<bf16_t>(bf16_t* to, const float (&v)[8]) {
+    v4u_t packed;
+#pragma unroll
+    for (int c = 0; c < 4; c++) packed[c] = (uint32_t)bf16_from_float(v[2 * c]).bits | ((uint32_t)bf16_from_float(v[2 * c + 1]).bits << 16);
+    __builtin_nontemporal_store(packed, reinterpret_cast<v4u_t*>(to));
+}
+
+template <int FM, int FN, int NB, int WAVES, int STEPS, int DEPTH, typename OutT, int EPI>
+__global__ __launch_bounds__(WAVES * 64) void split_kernel(
+    const int8_t* __restrict__ x, const int8_t* __restrict__ w, OutT* __restrict__ out, Epilogue e, int M, int N, int K)
+{
+    constexpr int BM = 32 * FM, BN = 32 * FN, THREADS = WAVES * 64, ROW = BN + 4;
+    constexpr bool RAW = std::is_same<OutT, int>::value;
+    constexpr int ROW_LANES = BN / 8, ROWS = THREADS / ROW_LANES, PASSES = (BM + ROWS - 1) / ROWS;
+    static_assert(STEPS >= 1 && DEPTH >= 1 && THREADS % ROW_LANES == 0, "split shape");
+    extern __shared__ __align__(16) int8_t lds[];
+    int* partial = (int*)lds;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int flags = EPI >= 0 ? EPI : e.flags;
+    const int tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
+    const int tile = xcd_local_tile(blockIdx.x, tiles_m * tiles_n);
+    constexpr int GROUP_M = 8;
+    const int in_group = GROUP_M * tiles_n;
+    const int first_m = tile / in_group * GROUP_M;
+    const int group_rows = min(tiles_m - first_m, GROUP_M);
+    const int m0 = (first_m + tile % in_group % group_rows) * BM;
+    const int n0 = (tile % in_group / group_rows) * BN;
+
+    // The epilogue's operands in the row layout, loaded now so that they arrive while the sums are made, and kept as raw
+    // bits until the epilogue: 8 columns' weight scales (of each row group) and bias, and each pass's row scale,
+    // residual and original row. Places past the edge read the last row or column (never stored).
+    const int n_local = (tid % ROW_LANES) * 8, n = n0 + n_local, n_read = min(n, N - 8);
+    v4u_t scales[NB][2];
+    uint2 bias[2] = {};
+    uint32_t row_scale[PASSES];
+    v4u_t residual[PASSES], original[PASSES];
+    if constexpr (!RAW) {
+#pragma unroll
+        for (int g = 0; g < NB; g++)
+#pragma unroll
+            for (int h = 0; h < 2; h++) scales[g][h] = *reinterpret_cast<const v4u_t*>(e.w_scale + (size_t)g * N + n_read + 4 * h);
+        if (flags & EPI_BIAS) {
+            bias[0] = *reinterpret_cast<const uint2*>(e.bias + n_read);
+            bias[1] = *reinterpret_cast<const uint2*>(e.bias + n_read + 4);
+        }
+#pragma unroll
+        for (int p = 0; p < PASSES; p++) {
+            const int m_read = min(m0 + min(p * ROWS + tid / ROW_LANES, BM - 1), M - 1);
+            row_scale[p] = __float_as_uint(e.x_scale[m_read]);
+            if (flags & EPI_RESIDUAL) residual[p] = *reinterpret_cast<const v4u_t*>(e.residual + (size_t)m_read * N + n_read);
+            if (flags & EPI_MIX) original[p] = *reinterpret_cast<const v4u_t*>(e.original + (size_t)m_read * N + n_read);
+        }
+    }
+    uint16_t mix_scales[2] = {0, 0};
+    if (!RAW && (flags & EPI_MIX)) {
+        mix_scales[0] = __builtin_bit_cast(uint16_t, e.residual_scale[0]);
+        mix_scales[1] = __builtin_bit_cast(uint16_t, e.input_scale[0]);
+    }
+
+    // this lane's operand rows (row lane % 32 of each fragment) at its 64 bytes of this wavefront's first step
+    const int r = lane & 31;
+    const size_t k_first = (size_t)wave * STEPS * CHUNK + (lane >> 5) * 64;
+    const int8_t* a_source[FM];
+    const int8_t* b_source[NB][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++) a_source[i] = x + (size_t)min(m0 + i * 32 + r, M - 1) * K + k_first;
+#pragma unroll
+    for (int g = 0; g < NB; g++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) b_source[g][j] = w + ((size_t)g * N + min(n0 + j * 32 + r, N - 1)) * K + k_first;
+
+    constexpr int BUFFERS = DEPTH < STEPS ? DEPTH : STEPS;
+    v4i a[BUFFERS][FM][4], b[BUFFERS][NB][FN][4];
+    auto load = [&](auto step_c) {
+        constexpr int S = decltype(step_c)::value, B = S % BUFFERS;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+#pragma unroll
+            for (int g = 0; g < NB; g++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) b[B][g][j][c] = *reinterpret_cast<const v4i*>(b_source[g][j] + S * CHUNK + 16 * c);
+#pragma unroll
+            for (int i = 0; i < FM; i++) a[B][i][c] = *reinterpret_cast<const v4i*>(a_source[i] + S * CHUNK + 16 * c);
+        }
+    };
+    v16i_t acc[NB][FM][FN];
+    static_for<0, BUFFERS>([&](auto s) { load(s); });
+    static_for<0, STEPS>([&](auto step_c) {
+        constexpr int S = decltype(step_c)::value, B = S % BUFFERS;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int g = 0; g < NB; g++)
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int i = 0; i < FM; i++)
+                        acc[g][i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(b[B][g][j][c], a[B][i][c],
+                                                                            S == 0 && c == 0 ? v16i_t{} : acc[g][i][j], 0, 0, 0);
+        if constexpr (S + BUFFERS < STEPS) load(std::integral_constant<int, S + BUFFERS>{});
+    });
+
+    // the partial tile: a lane holds row lane % 32 of a fragment and, in register 4 q + t, column 8 q + 4 (lane / 32) + t
+    int* mine = partial + wave * NB * BM * ROW;
+#pragma unroll
+    for (int g = 0; g < NB; g++)
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    *reinterpret_cast<v4i*>(mine + (g * BM + i * 32 + r) * ROW + j * 32 + 8 * q + 4 * (lane >> 5)) =
+                        v4i{acc[g][i][j][4 * q], acc[g][i][j][4 * q + 1], acc[g][i][j][4 * q + 2], acc[g][i][j][4 * q + 3]};
+    __syncthreads();
+
+#pragma unroll
+    for (int g = 0; g < NB; g++)
+#pragma unroll
+        for (int h = 0; h < 2; h++) asm volatile("" : "+v"(scales[g][h]));
+    asm volatile("" : "+v"(bias[0]), "+v"(bias[1]), "+v"(mix_scales[0]), "+v"(mix_scales[1]));
+    const float rs = (float)__builtin_bit_cast(half_t, mix_scales[0]), is = (float)__builtin_bit_cast(half_t, mix_scales[1]);
+#pragma unroll
+    for (int p = 0; p < PASSES; p++) {
+        const int m_local = p * ROWS + tid / ROW_LANES, m = m0 + m_local;
+        if ((BM % ROWS != 0 && m_local >= BM) || m >= M || n >= N) continue;
+        int sums[NB][8];
+#pragma unroll
+        for (int g = 0; g < NB; g++) {
+#pragma unroll
+            for (int c = 0; c < 8; c++) sums[g][c] = 0;
+#pragma unroll
+            for (int v = 0; v < WAVES; v++) {
+                const int* from = partial + ((v * NB + g) * BM + m_local) * ROW + n_local;
+                const v4i lo = *reinterpret_cast<const v4i*>(from), hi = *reinterpret_cast<const v4i*>(from + 4);
+#pragma unroll
+                for (int c = 0; c < 4; c++) {
+                    sums[g][c] += lo[c];
+                    sums[g][4 + c] += hi[c];
+                }
+            }
+        }
+        const size_t at = (size_t)m * N + n;
+        if constexpr (RAW) {
+            *reinterpret_cast<v4i*>(out + at) = v4i{sums[0][0], sums[0][1], sums[0][2], sums[0][3]};
+            *reinterpret_cast<v4i*>(out + at + 4) = v4i{sums[0][4], sums[0][5], sums[0][6], sums[0][7]};
+        } else {
+            asm volatile("" : "+v"(row_scale[p]));
+            const float xs = __uint_as_float(row_scale[p]);
+            float value[8];
+#pragma unroll
+            for (int c = 0; c < 8; c++) {
+                value[c] = ((float)sums[0][c] * xs) * __uint_as_float(scales[0][c / 4][c % 4]);
+                if (flags & EPI_BIAS) {
+                    const uint32_t word = c < 4 ? (c < 2 ? bias[0].x : bias[0].y) : (c < 6 ? bias[1].x : bias[1].y);
+                    value[c] = value[c] + (float)__builtin_bit_cast(half_t, (uint16_t)(word >> (16 * (c & 1))));
+                }
+                if constexpr (NB == 2) {
+                    const float up = ((float)sums[1][c] * xs) * __uint_as_float(scales[1][c / 4][c % 4]);
+                    value[c] = silu_fast(value[c]) * up;
+                }
+            }
+            if (flags & EPI_RESIDUAL) {
+                asm volatile("" : "+v"(residual[p]));
+                const v8h rows = __builtin_bit_cast(v8h, residual[p]);
+#pragma unroll
+                for (int c = 0; c < 8; c++) value[c] = value[c] + (float)rows[c];
+            }
+            if (flags & EPI_MIX) {
+                asm volatile("" : "+v"(original[p]));
+                const v8h rows = __builtin_bit_cast(v8h, original[p]);
+#pragma unroll
+                for (int c = 0; c < 8; c++) value[c] = (to_float(from_float<OutT>(value[c])) * rs) + ((float)rows[c] * is);
+            }
+            // the f32 value is what rounds: keep its last operation out of the conversion (one rounding, not two)
+#pragma unroll
+            for (int c = 0; c < 8; c++) asm volatile("" : "+v"(value[c]));
+            store_eight<OutT>(out + at, value);
+        }
+    }
+}
+
+// A split tile for K = STEPS x WAVES x 128 bytes, STEPS fixed at compile time (1, 2 or 4 a wavefront).
+template <int FM, int FN, int NB, int WAVES, int DEPTH, typename OutT, int EPI>
+int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, hipStream_t stream) {
+    if (N % 8 != 0) return chess_fail(CHESS_UNSUPPORTED, "a split-K tile writes 8 columns a lane: N %d is not a multiple of 8", N);
+    const int steps = K % (CHUNK * WAVES) == 0 ? K / (CHUNK * WAVES) : 0;
+    constexpr int BYTES = lds_bytes<FM, FN, NB, WAVES>();
+    const int tiles = ((M + 32 * FM - 1) / (32 * FM)) * ((N + 32 * FN - 1) / (32 * FN));
+    auto go = [&](auto kernel) {
+        if (BYTES > 65536) {
+            static const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, BYTES);
+            if (allowed != hipSuccess) return (int)allowed;
+        }
+        hipLaunchKernelGGL(kernel, dim3(tiles), dim3(WAVES * 64), BYTES, stream, (const int8_t*)x, (const int8_t*)w, (OutT*)out, e, M, N, K);
+        return launch_status();
+    };
+    switch (steps) {
+        case 1: return go(split_kernel<FM, FN, NB, WAVES, 1, DEPTH, OutT, EPI>);
+        case 2: return go(split_kernel<FM, FN, NB, WAVES, 2, DEPTH, OutT, EPI>);
+        case 4: return go(split_kernel<FM, FN, NB, WAVES, 4, DEPTH, OutT, EPI>);
+        default:
+            return chess_fail(CHESS_UNSUPPORTED, "a split-K tile of %d wavefronts reads rows of %d, %d or %d bytes, not %d", WAVES,
+                              CHUNK * WAVES, 2 * CHUNK * WAVES, 4 * CHUNK * WAVES, K);
+    }
+}
+
+// The split tile: 14, 32 x 32 outputs over 4 wavefronts (each 1, 2 or 4 steps of K). In a kernel trace it takes 3.6 us
+// where the whole-K 64 x 64 tile takes 4.4 (projection, 70 rows), 4.3 against 5.2 (gate_up) and 6.2 against 7.6 (down);
+// from about 200 rows on the whole-K tiles are faster.
+template <int NB, typename OutT, int EPI>
+int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    if (tile == FIRST_SPLIT) return launch<1, 1, NB, 4, 2, OutT, EPI>(x, w, out, e, M, N, K, stream);
+    return chess_fail(CHESS_UNSUPPORTED, "tile %d is not a split-K tile", tile);
+}
+
+// The network's epilogues with their flags fixed at compile time (fp16 out), any other combination read at run time.
+template <int NB, typename OutT>
+int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
+    const int f = e.flags;
+    if constexpr (std::is_same<OutT, half_t>::value) {
+        if constexpr (NB == 2) {
+            if (f == 0) return by_tile<NB, OutT, 0>(x, w, out, e, M, N, K, tile, stream);
+        } else {
+            if (f == EPI_BIAS) return by_tile<NB, OutT, EPI_BIAS>(x, w, out, e, M, N, K, tile, stream);
+            if (f == EPI_RESIDUAL) return by_tile<NB, OutT, EPI_RESIDUAL>(x, w, out, e, M, N, K, tile, stream);
+            if (f == (EPI_RESIDUAL | EPI_MIX)) return by_tile<NB, OutT, EPI_RESIDUAL | EPI_MIX>(x, w, out, e, M, N, K, tile, stream);
+        }
+    }
+    return by_tile<NB, OutT, -1>(x, w, out, e, M, N, K, tile, stream);
+}
+
+}  // namespace split

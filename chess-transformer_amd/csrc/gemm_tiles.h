@@ -35,6 +35,7 @@
 #pragma once
 
 #include "gemm.h"
+#include "gemm_split.h"
 #include "lds_dma.h"
 
 #include <type_traits>
@@ -500,6 +501,10 @@ template <typename In, int NB, typename OutT>
 int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     if (tile == 0) tile = tile_by_size<In>(M, N, K);
     if (tile == 12) return chess_fail(CHESS_UNSUPPORTED, "tile 12 is not a tile of this GEMM");
+    if (tile >= FIRST_SPLIT) {
+        if constexpr (std::is_same<In, int8_t>::value) return split::dispatch<NB, OutT>(x, w, out, e, M, N, K, tile, stream);
+        return chess_fail(CHESS_UNSUPPORTED, "the split-K tile %d is int8 only", FIRST_SPLIT);
+    }
     const int f = e.flags;
     if constexpr (sizeof(OutT) == 2) {
         if (f == 0) return by_tile<In, NB, OutT, true, 0>(x, w, out, e, M, N, K, tile, stream);

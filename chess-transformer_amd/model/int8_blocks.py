@@ -15,7 +15,7 @@ import torch
 from torch import nn
 
 from model import hip_kernels
-from model.fused_blocks import FusedBlock, linear, link_input_mixes, template_attention, tile_for
+from model.fused_blocks import FusedBlock, linear, link_input_mixes, template_attention
 from model.hip_kernels import aligned, check, library_for, pointer, stream_of
 
 # model/int8_blocks.py:14-17 of the reference: the mlp's hidden is rotated in blocks of 32 (H H^T = 32 I) and
@@ -27,10 +27,15 @@ INT8_DEPTH = 64
 # MI355X: 1 is 64 x 64, 2 128 x 128, 3 128 x 64, 4 256 x 128, 5 128 x 256, 6 256 x 64 (rows x outputs, a 4-stage ring),
 # 7 128 x 128, 8 128 x 64, 9 256 x 64 (a 3-stage ring), 10 256 x 64, 11 128 x 128 (a 2-stage ring: three workgroups a
 # compute unit, which is what the batch-1024 network runs fastest with), 13 128 x 128 (a 2-stage ring of 128-byte stages:
-# down's 2,048-byte rows, read in whole L2 lines). Every tile gives the same bits.
-INT8_TILES = {"gfx950": {"projection": [(4, 1), (math.inf, 11)],
-                         "gate_up": [(4, 1), (math.inf, 10)],
-                         "down": [(32, 1), (math.inf, 13)]}}
+# down's 2,048-byte rows, read in whole L2 lines), 14 32 x 32 with K split over 4 wavefronts (the reference's small_int8
+# for one or two positions, int8_cuda.py:34-183: in a kernel trace 3.6, 4.3 and 6.2 us where tile 1 takes 4.4, 5.2 and 7.6
+# for projection, gate_up and down at 70 rows; gate_up's tile 1 is faster again at 140 rows, the others from about 200).
+# Every tile gives the same bits.
+INT8_TILES = {"gfx950": {"projection": [(0.55, 14), (4, 1), (math.inf, 11)],
+                         "gate_up": [(0.3, 14), (4, 1), (math.inf, 10)],
+                         "down": [(0.55, 14), (32, 1), (math.inf, 13)]}}
+# the split-K tile's wavefronts: each reads 1, 2 or 4 steps of 128 bytes of K, and the outputs go 8 columns a lane
+SPLIT_WAVES = {14: 4}
 # rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit
 NORM_ROWS = 4
 ROTATE_ROWS = 4
@@ -40,10 +45,20 @@ def gpu_arch(device: torch.device) -> str:
     return torch.cuda.get_device_properties(device).gcnArchName.split(":")[0]
 
 
-def int8_tile(device: torch.device, matmul: str, M: int) -> int:
-    """The tile of int8_linear for M rows of matmul (reference int8_blocks.py:39-42, keyed by gfx target, not capability)."""
+def split_takes(tile: int, N: int, K: int) -> bool:
+    """Whether split-K tile takes N outputs of depth K (the whole-K tiles take every shape int8_linear takes)."""
+    waves = SPLIT_WAVES.get(tile)
+    return waves is None or (N % 8 == 0 and K % (128 * waves) == 0 and K // (128 * waves) in (1, 2, 4))
+
+
+def int8_tile(device: torch.device, matmul: str, M: int, N: int = 0, K: int = 0) -> int:
+    """The tile of int8_linear for M rows of matmul (reference int8_blocks.py:39-42, keyed by gfx target, not capability):
+    the table's entry for the rows a compute unit's share is, or, given N and K, the first entry from there on whose tile
+    takes them."""
     tiles = INT8_TILES.get(gpu_arch(device), INT8_TILES["gfx950"])[matmul]
-    return tile_for(tiles, M, torch.cuda.get_device_properties(device).multi_processor_count)
+    share = M / torch.cuda.get_device_properties(device).multi_processor_count
+    candidates = [tile for most, tile in tiles if share <= most]
+    return next((tile for tile in candidates if not N or split_takes(tile, N, K)), candidates[-1])
 
 
 def rotate_rows(device: torch.device, M: int) -> int:
@@ -127,7 +142,8 @@ def int8_matmul_i32(x: torch.Tensor, weight: torch.Tensor, tile: int = 0) -> tor
 def int8_linear(x: torch.Tensor, x_scale: torch.Tensor, weight: torch.Tensor, weight_scale: torch.Tensor, bias: torch.Tensor | None,
                 residual: torch.Tensor | None, gated: bool, matmul: str, original: torch.Tensor | None = None,
                 residual_scale: torch.Tensor | None = None, input_scale: torch.Tensor | None = None) -> torch.Tensor:
-    tile = int8_tile(x.device, matmul, x.numel() // weight.shape[1])
+    rows, K = weight.shape
+    tile = int8_tile(x.device, matmul, x.numel() // K, rows // 2 if gated else rows, K)
     return launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, original, residual_scale, input_scale, tile)
 
 

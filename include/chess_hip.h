@@ -47,7 +47,8 @@ int chess_rotate_quant(const void* h, void* q, void* scale, int M, int N, int wi
  * + residual[M, N], then the next block's input mix when original != NULL; fp16 or bf16 out.
  * K % 64 == 0. tile: 0 picks by size; 1..11 force 64x64, 128x128, 128x64, 256x128, 128x256, 256x64 (rows x
  * outputs), then 128x128, 128x64, 256x64 with a 3-stage ring and 256x64, 128x128 with a 2-stage ring; 13 128x128
- * with 128-byte stages (K a multiple of 128 bytes); 12 is refused. No tile changes a bit.
+ * with 128-byte stages (K a multiple of 128 bytes); 12 is refused; 14 32x32 with K split over 4 wavefronts, for few
+ * rows (K = 512, 1024 or 2048 and N % 8 == 0: the role of small_int8). No tile changes a bit.
  * Pointer order of small_int8 (model/int8_cuda.py:35-39); replaces int8_linear_kernel
  * and small_int8 (model/int8_blocks.py:66-144, model/int8_cuda.py:34-183, :362-383). */
 int chess_int8_linear(const void* x, const void* x_scale, const void* w, const void* w_scale, const void* bias, const void* residual,

@@ -167,10 +167,38 @@ def test_int8_sums_are_exact(device, M, N, K, tile):
     assert found.dtype == torch.int32 and torch.equal(found.cpu().long(), expected)
 
 
+@pytest.mark.parametrize("M, N, K", [(1, 200, 512), (70, 1600, 512), (140, 512, 2048), (1120, 512, 2048), (333, 64, 1024), (4480, 2048, 512),
+                                     (70, 96, 256)])
+@pytest.mark.parametrize("tile", [14])
+def test_the_split_k_sums_are_exact(device, M, N, K, tile):
+    """The split-K tile's int32 sums, the partial tiles of 4 wavefronts added in LDS, at one to 4,480 rows (ragged last
+    row and column tiles); a depth its wavefronts cannot split in 1, 2 or 4 steps of 128 bytes is refused."""
+    generator = torch.Generator(device="cpu").manual_seed(M + N + K + tile)
+    x = torch.randint(-127, 128, (M, K), generator=generator, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=generator, dtype=torch.int8)
+    if not int8_blocks.split_takes(tile, N, K):
+        with pytest.raises(ValueError):
+            int8_matmul_i32(x.to(device), w.to(device), tile)
+        return
+    found = int8_matmul_i32(x.to(device), w.to(device), tile)
+    assert found.dtype == torch.int32 and torch.equal(found.cpu().long(), x.long() @ w.long().T)
+
+
+def test_the_split_k_tiles_refuse_what_they_cannot_take(device):
+    """The split tile writes 8 columns a lane and takes int8 only: N % 8 != 0 and the fp16 instance are refused."""
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("projection", 70, device, width=196)
+    launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 1)
+    for tile in SPLIT_TILES:
+        with pytest.raises(ValueError):
+            launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
+        with pytest.raises(ValueError):
+            launch_linear(x.half(), (weight.float().t() / 128).half().contiguous(), bias, None, False, False, None, None, None, tile)
+
+
 def int8_operands(matmul: str, rows: int, device, width: int = 200, depth: int | None = None):
     torch.manual_seed(rows + width)
     down, gated = matmul.endswith("down"), matmul == "gate_up"
-    depth = depth or (1024 if down else 256)
+    depth = depth or (1024 if down else 512)
     x = torch.randint(-127, 128, (rows, depth), device=device, dtype=torch.int8)
     x_scale = torch.rand(rows, device=device) / 100
     weight = torch.randint(-127, 128, (2 * width if gated else width, depth), device=device, dtype=torch.int8)
@@ -215,7 +243,7 @@ def test_the_gated_epilogue_is_silu_times_up(device, rows):
 
 
 def same_bits(found: torch.Tensor, expected: torch.Tensor) -> bool:
-    as_integers = {torch.float16: torch.int16, torch.float32: torch.int32}
+    as_integers = {torch.float16: torch.int16, torch.bfloat16: torch.int16, torch.float32: torch.int32}
     return found.shape == expected.shape and found.dtype == expected.dtype and torch.equal(
         found.view(as_integers.get(found.dtype, found.dtype)), expected.view(as_integers.get(expected.dtype, expected.dtype)))
 
@@ -230,7 +258,7 @@ def test_int8_linear_is_the_dequantised_matmul(device, matmul, boards):
     """The reference's check (tests/test_int8.py:59-90): every tile, rows and columns leaving tiles part empty."""
     torch.manual_seed(0)
     down, gated = matmul.endswith("down"), matmul == "gate_up"
-    width, depth = 200, 1024 if down else 256
+    width, depth = 200, 1024 if down else 512
     x = torch.randint(-127, 128, (boards, 70, depth), device=device, dtype=torch.int8)
     x_scale = torch.rand(boards, 70, device=device) / 100
     weight = torch.randint(-127, 128, (2 * width if gated else width, depth), device=device, dtype=torch.int8)
@@ -265,6 +293,17 @@ def test_int8_linear_writes_bf16(device):
     assert np.array_equal(cpu(out.float()), expected)
 
 
+@pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.bfloat16])
+def test_the_split_k_tiles_give_the_whole_k_tiles_bits(device, matmul, out_dtype):
+    """Split-K against whole-K tiles at 70 rows (one position), every epilogue (the gated one too) in fp16 and bf16."""
+    x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands(matmul, 70, device, width=1600 if matmul == "projection" else 512)
+    expected = launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 1, out_dtype)
+    for tile in SPLIT_TILES:
+        if int8_blocks.split_takes(tile, expected.shape[-1], x.shape[-1]):
+            assert same_bits(launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile, out_dtype), expected), tile
+
+
 def config1_case(M: int, K: int, N: int, device):
     """A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02) (a scale a row), f32 row scales,
     bias N(0, 0.02), bf16 out."""
@@ -297,14 +336,16 @@ def test_the_config1_gemms_are_the_oracles_in_bf16(device, M, K, N):
 
 
 ALL_TILES = (*range(1, 12), 13)   # 12 is not a tile; 13 takes 128-byte stages
+SPLIT_TILES = (14,)              # int8 only
 
 
 @pytest.mark.parametrize("matmul", ["projection", "gate_up", "down", "mixing down"])
 def test_every_tile_gives_the_same_bits(device, matmul):
-    """Every tile of the int8 GEMM and of its fp16 instance, partial last tiles in rows (210) and columns (200): one set of bits."""
+    """Every tile of the int8 GEMM (the split-K ones included) and of its fp16 instance, partial last tiles in rows (210) and
+    columns (200): one set of bits."""
     operands = int8_operands(matmul, 210, device)
     x, x_scale, weight, weight_scale, bias, residual, gated, mix = operands
-    outputs = [launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile) for tile in ALL_TILES]
+    outputs = [launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile) for tile in (*ALL_TILES, *SPLIT_TILES)]
     assert all(same_bits(out, outputs[0]) for out in outputs[1:])
     halves = x.half()
     w16 = (weight.float().t() / 128).half().contiguous()

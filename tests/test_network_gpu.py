@@ -170,8 +170,8 @@ def test_tiles_change_no_answer(device, monkeypatch):
     network = int8_network(make_model().to(device), nearest_int8_weights(make_model()))
     with torch.no_grad():
         answers = [answer_rows(network(random_boards(size, seed=size).to(device))) for size in (1, 3, 16)]
-        for module in (fused_blocks, int8_blocks):
-            monkeypatch.setattr(module, "tile_for", lambda tiles, M, multiprocessors: tiles[-1][1])
+        monkeypatch.setattr(fused_blocks, "tile_for", lambda tiles, M, multiprocessors: tiles[-1][1])
+        monkeypatch.setattr(int8_blocks, "int8_tile", lambda device, matmul, M, N=0, K=0: int8_blocks.INT8_TILES["gfx950"][matmul][-1][1])
         forced = [answer_rows(network(random_boards(size, seed=size).to(device))) for size in (1, 3, 16)]
     assert all(torch.equal(a, b) for a, b in zip(answers, forced))
 
