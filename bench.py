@@ -9,6 +9,8 @@ baseline (the CPU oracle's fp32 forward, the reference's CPU path, on a bounded 
 python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch 1024] [--sweep] [--no-cpu]
 python bench.py --kernel-only      the dominant kernel and a plain copy alone, for rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE
 python bench.py --pmc-summary DIR  reads those two runs' counter_collection.csv files and prints the HBM bytes per launch
+python bench.py --network-only     eager forwards of the network at --batch (no graph, no timing), for rocprofv3 --pmc runs
+                                   whose counters are summarised per kernel by --counter-summary DIR
 """
 from __future__ import annotations
 
@@ -34,7 +36,7 @@ TOKENS = 70
 GEMM_TILES = {1: "64x64, 4 waves, 4 stages", 2: "128x128, 4 waves, 4 stages", 3: "128x64, 4 waves, 4 stages", 4: "256x128, 4 waves, 3 stages",
               5: "128x256, 4 waves, 3 stages", 6: "256x64, 4 waves, 4 stages", 7: "128x128, 4 waves, 3 stages", 8: "128x64, 4 waves, 3 stages",
               9: "256x64, 4 waves, 3 stages", 10: "256x64, 4 waves, 2 stages", 11: "128x128, 4 waves, 2 stages",
-              13: "128x128, 4 waves, 2 stages of 128 bytes"}
+              13: "128x128, 4 waves, 2 stages of 128 bytes", 14: "32x32, K split over 4 waves"}
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a plain copy's counters
 TRAFFIC = ROOT / "profiles" / "gate_up_gemm_batch1024_traffic.json"
 COPY_BYTES = 1 << 29
@@ -284,6 +286,106 @@ def kernel_only(batch: int, repeats: int = 20) -> int:
     return 0
 
 
+def network_only(batch: int, passes: int = 2) -> int:
+    """Eager forwards of the d512 x 28 network at batch (one untimed, then passes), for rocprofv3 --pmc runs: every kernel of a
+    forward is a dispatch of its own, so the counters come per kernel. A copy of COPY_BYTES follows, for FETCH_SIZE / WRITE_SIZE's
+    scale."""
+    import torch
+    from engine.inference import int8_network
+    from engine.quantization import nearest_int8_weights
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    model = synthetic_model(SETTINGS)
+    network = int8_network(model.to(device), nearest_int8_weights(model))
+    boards = legal_boards(batch).to(device)
+    with torch.no_grad():
+        for _ in range(1 + passes):
+            network(boards)
+    source = torch.empty(COPY_BYTES, device=device, dtype=torch.uint8).random_(0, 255)
+    torch.empty_like(source).copy_(source)
+    torch.cuda.synchronize()
+    log(f"network-only: {1 + passes} eager forwards at batch {batch}, then a copy of {COPY_BYTES} bytes")
+    return 0
+
+
+def kernel_role(name: str) -> str:
+    """The network's part a kernel plays, from its (mangled) name: the GEMM's template arguments tell the int8 matmuls apart by
+    their operand type, weight row groups (2: gated) and epilogue flags."""
+    import re
+    if "gemm_kernel" in name or "split_kernel" in name:
+        found = re.search(r"(?:gemm|split)_kernelI(a|DF16_)?((?:Li\d+E)+)(DF16_|DF16b|f|i)?Lb(\d)ELi(n?\d+)E", name)
+        numbers = [int(v) for v in re.findall(r"Li(\d+)E", found.group(2))] if found else []
+        if "split_kernel" in name:
+            found = re.search(r"split_kernelI((?:Li\d+E)+)(DF16_|DF16b|i)Li(n?\d+)E", name)
+            numbers = [int(v) for v in re.findall(r"Li(\d+)E", found.group(1))] if found else []
+            nb, epilogue = (numbers[2] if len(numbers) > 2 else 1), (found.group(3) if found else "?")
+            return {"2": "down (split-K)", "6": "down (split-K)", "1": "projection (split-K)"}.get(epilogue, "gate_up (split-K)" if nb == 2 else "int8 split-K")
+        if not found:
+            return "gemm"
+        int8 = found.group(1) == "a"
+        nb = numbers[4] if len(numbers) > 4 else 1
+        epilogue = found.group(5)
+        out = found.group(3)
+        if int8:
+            if nb == 2:
+                return "gate_up (int8, gated)"
+            return {"1": "projection (int8)", "2": "down (int8)", "6": "down (int8, mixes the next input)"}.get(epilogue, "int8 gemm")
+        if out == "f":
+            return "policy head a (fp16, f32 out)"
+        if nb == 2:
+            return "fp16 block gate_up"
+        return {"3": "combine (fp16, bias + residual)", "1": "fp16 block projection", "2": "fp16 block down",
+                "6": "fp16 block down (mix)"}.get(epilogue, "fp16 gemm")
+    for key, role in (("norm_quant_kernel", "norm_quant"), ("rotate_quant", "rotate_quant"), ("template_attention", "template_attention"),
+                      ("board_embedding", "board_embedding"), ("move_logits", "move_logits"), ("value_hidden", "value_hidden"),
+                      ("value_score", "value_score"), ("copy", "copy")):
+        if key in name:
+            return role
+    return name.split("<")[0][:60]
+
+
+def counter_summary(folder: Path) -> int:
+    """Per kernel role, the average per dispatch of every counter in the rocprofv3 --pmc runs under folder (their
+    counter_collection.csv files), as a markdown table, with derived figures. GRBM_GUI_ACTIVE is summed over the 8 XCDs, so a
+    dispatch's cycles are GRBM_GUI_ACTIVE / 8. From those: int8 MFMA % = 512 SQ_INSTS_VALU_MFMA_MOPS_I8 over the dense peak at
+    the running clock (256 CUs x 4 SIMDs x 2,048 ops a cycle); MFMA busy % = SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1,024 SIMDs);
+    VALU busy % = 4 SQ_ACTIVE_INST_VALU / (cycles x 1,024) (the SQ's wave counters count 4-cycle units); co-exec % = the MFMA
+    busy cycles that VALU work overlaps; L2 requests a cycle a channel (128 channels); per wavefront, its VALU and MFMA
+    instructions and its cycles spent waiting."""
+    import csv
+    values: dict[str, dict[str, list[float]]] = {}
+    for path in sorted(folder.rglob("*counter_collection.csv")):
+        for row in csv.DictReader(path.open()):
+            values.setdefault(kernel_role(row["Kernel_Name"]), {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+    columns = ["dispatch cycles", "int8 MFMA % of peak", "MFMA busy %", "VALU busy %", "MFMA co-exec with VALU %",
+               "L2 requests /cycle/channel", "L2 hit %", "TA busy %", "VALU instr /wave", "MFMA instr /wave", "transcendental /wave",
+               "waiting cycles /wave", "wave cycles /wave", "FETCH_SIZE KiB", "WRITE_SIZE KiB"]
+    print("| kernel | dispatches | " + " | ".join(columns) + " |")
+    print("|---|---|" + "---|" * len(columns))
+    for role in sorted(values):
+        mean = {counter: sum(v) / len(v) for counter, v in values[role].items()}
+        dispatches = max(len(v) for v in values[role].values())
+        cycles = mean.get("GRBM_GUI_ACTIVE", 0) / 8
+        waves = mean.get("SQ_WAVES")
+
+        def ratio(top, bottom, scale=1.0, digits=1):
+            return f"{scale * top / bottom:,.{digits}f}" if top is not None and bottom else ""
+        cells = [f"{cycles:,.0f}" if cycles else "",
+                 ratio(mean.get("SQ_INSTS_VALU_MFMA_MOPS_I8"), cycles * 2097152, 512 * 100),
+                 ratio(mean.get("SQ_VALU_MFMA_BUSY_CYCLES"), cycles * 1024, 100),
+                 ratio(mean.get("SQ_ACTIVE_INST_VALU"), cycles * 1024, 400),
+                 ratio(mean.get("SQ_VALU_MFMA_COEXEC_CYCLES"), mean.get("SQ_VALU_MFMA_BUSY_CYCLES"), 100),
+                 ratio(mean.get("TCC_REQ_sum"), cycles * 128, 1, 2),
+                 ratio(mean.get("TCC_HIT_sum"), (mean.get("TCC_HIT_sum") or 0) + (mean.get("TCC_MISS_sum") or 0), 100),
+                 ratio(mean.get("TA_BUSY_avr"), cycles, 100),
+                 ratio(mean.get("SQ_INSTS_VALU"), waves, 1, 0), ratio(mean.get("SQ_INSTS_MFMA"), waves, 1, 0),
+                 ratio(mean.get("SQ_INSTS_VALU_TRANS_F32"), waves, 1, 0), ratio(mean.get("SQ_WAIT_ANY"), waves, 4, 0),
+                 ratio(mean.get("SQ_WAVE_CYCLES"), waves, 4, 0),
+                 f"{mean['FETCH_SIZE']:,.0f}" if "FETCH_SIZE" in mean else "", f"{mean['WRITE_SIZE']:,.0f}" if "WRITE_SIZE" in mean else ""]
+        print(f"| {role} | {dispatches} | " + " | ".join(cells) + " |")
+    return 0
+
+
 def pmc_summary(folder: Path, batch: int) -> int:
     """HBM bytes per launch of the dominant kernel from two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, KiB per dispatch), each
     scaled by what the counter reads for the copy of COPY_BYTES."""
@@ -393,15 +495,21 @@ def main() -> int:
     parser.add_argument("--no-standalone", action="store_true", help="skip the standalone GEMM and attention configs")
     parser.add_argument("--kernel-only", action="store_true", help="run only the dominant kernel and a copy, for counter runs")
     parser.add_argument("--pmc-summary", type=Path, help="summarise the FETCH_SIZE / WRITE_SIZE runs under this folder")
+    parser.add_argument("--network-only", action="store_true", help="eager forwards of the network at --batch, for counter runs")
+    parser.add_argument("--counter-summary", type=Path, help="per-kernel table of the counter runs under this folder")
     arguments = parser.parse_args()
     if arguments.pmc_summary:
         return pmc_summary(arguments.pmc_summary, arguments.batch)
+    if arguments.counter_summary:
+        return counter_summary(arguments.counter_summary)
     if arguments.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one and nothing in this build uses a second (asked for {arguments.gpus})",
               file=sys.stderr)
         return 2
     if arguments.kernel_only:
         return kernel_only(arguments.batch)
+    if arguments.network_only:
+        return network_only(arguments.batch)
 
     import torch
     from engine.inference import int8_network
@@ -467,7 +575,8 @@ def main() -> int:
     result = {"metric": "positions/sec at batch 1024 (28L int8 net)", "value": round(positions_per_s, 1), "unit": "positions/s", "n_gpus": 1,
               "steps": arguments.steps, "warmup": arguments.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
               "scaling": "weak", "vs_baseline": None, "dtype": "int8",
-              "data": "synthetic: random-init weights (N(0, 0.02)), round-to-nearest int8 per channel, random token boards",
+              "data": "synthetic: random-init weights (N(0, 0.02)), round-to-nearest int8 per channel, seeded random legal positions "
+                      "(tests/golden/positions.npz)",
               "config": {"workload": f"Fry int8 network d512 x 28 (27 int8 blocks + fp16 last), T=70, batch {arguments.batch}, HIP graph replay",
                          "batch": arguments.batch, "tokens": TOKENS, "d_model": 512, "layers": 28, "heads": 8, "mlp_hidden": 2048},
               "batch64": latency, "roofline": roofline, "cpu_baseline": baseline, **standalone}
