@@ -6,10 +6,11 @@
 // along each of 8 lines and how far out, the knights attacking it, the nearest pawn up and down its file.
 // The features are summed in f32 in their slot order (0..22), then rounded to fp16 (model/fused_blocks.py:383-393).
 //
-// A workgroup takes one board: its 64 squares' 23 rows are found by one thread a square into LDS, then
-// every (token, 8 columns) item gathers its rows 16 bytes a lane. Row numbers are clamped into the table
-// (and codes into the embedding), so that a board with codes the encoding never makes reads no memory
-// outside the tables.
+// A workgroup takes one board's run of TOKENS_A_GROUP tokens (9 workgroups a board of 70), so that a batch of one board
+// still spreads over the chip: it reads the whole board's codes and finds its kings and queens, then its squares' 23
+// rows with one thread a (square, direction), then gathers the rows of its (token, 8 columns) items, 16 bytes a lane,
+// two items a thread. Row numbers are clamped into the table (and codes into the embedding), so that a board with
+// codes the encoding never makes reads no memory outside the tables.
 #include "chess_common.h"
 
 namespace {
@@ -22,25 +23,27 @@ struct Codes {
     int pawn, knight, queen, king, theirs, edge, no_piece;
 };
 
+constexpr int TOKENS_A_GROUP = 8;
+constexpr int THREADS = 256;
+
 template <typename Code>
-__global__ __launch_bounds__(256) void board_embedding_kernel(
+__global__ __launch_bounds__(THREADS) void board_embedding_kernel(
     const Code* __restrict__ boards, const int* __restrict__ rays, const int* __restrict__ jumps, const int* __restrict__ offsets,
     const half_t* __restrict__ embed, const half_t* __restrict__ position, const half_t* __restrict__ table, half_t* __restrict__ out,
     int T, int D, int embed_rows, int table_rows, Codes codes)
 {
     __shared__ int square_codes[SQUARES + 1];     // the 65th is the code past the edge
-    __shared__ int token_codes[128];
+    __shared__ int token_codes[TOKENS_A_GROUP];
     __shared__ int first[4];
-    __shared__ int rows[SQUARES][FEATURES + 1];
+    __shared__ int rows[TOKENS_A_GROUP][FEATURES + 1];
 
     const int tid = threadIdx.x;
-    const size_t b = blockIdx.x;
+    const int groups = (T + TOKENS_A_GROUP - 1) / TOKENS_A_GROUP;
+    const size_t b = blockIdx.x / groups;
+    const int t0 = (blockIdx.x % groups) * TOKENS_A_GROUP;
     const Code* board = boards + b * T;
-    if (tid < T) {
-        const int code = (int)board[tid];
-        token_codes[tid] = min(max(code, 0), embed_rows - 1);
-        if (tid < SQUARES) square_codes[tid] = code;
-    }
+    if (tid < SQUARES) square_codes[tid] = (int)board[tid];
+    if (tid < TOKENS_A_GROUP) token_codes[tid] = t0 + tid < T ? min(max((int)board[t0 + tid], 0), embed_rows - 1) : 0;
     if (tid == SQUARES) square_codes[SQUARES] = codes.edge;
     if (tid < 4) first[tid] = SQUARES;
     __syncthreads();
@@ -52,54 +55,57 @@ __global__ __launch_bounds__(256) void board_embedding_kernel(
     }
     __syncthreads();
 
-    if (tid < SQUARES) {
-        const int s = tid, file = s % 8, rank = s / 8;
-        int row[FEATURES];
+    // thread (square of the group, direction d): the neighbour's code and the line's first piece along d, and for d < 2
+    // the nearest pawn along the file; direction 0's thread also the kings' and queens' places and the knights
+    const int local = tid / 8, d = tid % 8, s = t0 + local;
+    if (local < TOKENS_A_GROUP && s < min(T, SQUARES)) {
+        const int file = s % 8, rank = s / 8;
+        int* row = rows[local];
+        const int* ray = rays + (s * 8 + d) * STEPS;
+        int steps[STEPS];
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int p = first[i];
-            row[i] = p < SQUARES ? (rank - p / 8 + 7) * 15 + file - p % 8 + 7 : codes.no_piece;
-        }
+        for (int k = 0; k < STEPS; k++) steps[k] = ray[k];
         const int pawn_theirs = codes.pawn + codes.theirs;
+        int line = 0, pawn = 0;
+        bool line_found = false, pawn_found = false;
 #pragma unroll
-        for (int d = 0; d < 8; d++) {
-            const int* ray = rays + (s * 8 + d) * STEPS;
-            int line = 0, pawn = 0;
-            bool line_found = false, pawn_found = false;
-#pragma unroll
-            for (int k = 0; k < STEPS; k++) {
-                const int at = min(max(ray[k], 0), SQUARES);
-                const int code = square_codes[at];
-                if (k == 0) row[4 + d] = code;
-                if (!line_found && code != 0 && code != codes.edge) {
-                    line = 1 + (code - 1) * 7 + k;
-                    line_found = true;
-                }
-                if (d < 2 && !pawn_found && (code == codes.pawn || code == pawn_theirs)) {
-                    pawn = 1 + (code == pawn_theirs ? 7 : 0) + k;
-                    pawn_found = true;
-                }
+        for (int k = 0; k < STEPS; k++) {
+            const int code = square_codes[min(max(steps[k], 0), SQUARES)];
+            if (k == 0) row[4 + d] = min(max(code + offsets[4 + d], 0), table_rows - 1);
+            if (!line_found && code != 0 && code != codes.edge) {
+                line = 1 + (code - 1) * 7 + k;
+                line_found = true;
             }
-            row[12 + d] = line;
-            if (d < 2) row[21 + d] = pawn;
+            if (d < 2 && !pawn_found && (code == codes.pawn || code == pawn_theirs)) {
+                pawn = 1 + (code == pawn_theirs ? 7 : 0) + k;
+                pawn_found = true;
+            }
         }
-        int ours = 0, theirs = 0;
+        row[12 + d] = min(max(line + offsets[12 + d], 0), table_rows - 1);
+        if (d < 2) row[21 + d] = min(max(pawn + offsets[21 + d], 0), table_rows - 1);
+        if (d == 0) {
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const int code = square_codes[min(max(jumps[s * 8 + j], 0), SQUARES)];
-            ours += code == codes.knight;
-            theirs += code == codes.knight + codes.theirs;
+            for (int i = 0; i < 4; i++) {
+                const int p = first[i];
+                const int value = p < SQUARES ? (rank - p / 8 + 7) * 15 + file - p % 8 + 7 : codes.no_piece;
+                row[i] = min(max(value + offsets[i], 0), table_rows - 1);
+            }
+            int ours = 0, theirs = 0;
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int code = square_codes[min(max(jumps[s * 8 + j], 0), SQUARES)];
+                ours += code == codes.knight;
+                theirs += code == codes.knight + codes.theirs;
+            }
+            row[20] = min(max(min(ours, 2) * 3 + min(theirs, 2) + offsets[20], 0), table_rows - 1);
         }
-        row[20] = min(ours, 2) * 3 + min(theirs, 2);
-#pragma unroll
-        for (int f = 0; f < FEATURES; f++) rows[s][f] = min(max(row[f] + offsets[f], 0), table_rows - 1);
     }
     __syncthreads();
 
-    const int chunks = D / 8;
-    for (int item = tid; item < T * chunks; item += blockDim.x) {
-        const int token = item / chunks, d0 = (item % chunks) * 8;
-        const v8h e = *reinterpret_cast<const v8h*>(embed + (size_t)token_codes[token] * D + d0);
+    const int chunks = D / 8, tokens = min(TOKENS_A_GROUP, T - t0);
+    for (int item = tid; item < tokens * chunks; item += THREADS) {
+        const int local_token = item / chunks, token = t0 + local_token, d0 = (item % chunks) * 8;
+        const v8h e = *reinterpret_cast<const v8h*>(embed + (size_t)token_codes[local_token] * D + d0);
         const v8h p = *reinterpret_cast<const v8h*>(position + (size_t)token * D + d0);
         float total[8];
 #pragma unroll
@@ -108,7 +114,7 @@ __global__ __launch_bounds__(256) void board_embedding_kernel(
             float features[8] = {0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
             for (int f = 0; f < FEATURES; f++) {
-                const v8h t = *reinterpret_cast<const v8h*>(table + (size_t)rows[token][f] * D + d0);
+                const v8h t = *reinterpret_cast<const v8h*>(table + (size_t)rows[local_token][f] * D + d0);
 #pragma unroll
                 for (int c = 0; c < 8; c++) features[c] = features[c] + (float)t[c];
             }
@@ -139,6 +145,7 @@ extern "C" int chess_board_embedding(const void* boards, int code_bytes, const v
         return chess_fail(CHESS_MISALIGNED, "board_embedding's 16-byte loads need aligned tables and output");
     if (B == 0) return CHESS_OK;
     const Codes codes{pawn, knight, queen, king, theirs, edge, no_piece};
+    const long grid = (long)B * ((T + TOKENS_A_GROUP - 1) / TOKENS_A_GROUP);
     hipStream_t s = (hipStream_t)stream;
     const int* r = (const int*)rays;
     const int* j = (const int*)jumps;
@@ -146,11 +153,11 @@ extern "C" int chess_board_embedding(const void* boards, int code_bytes, const v
     const half_t *e = (const half_t*)embed, *p = (const half_t*)position, *t = (const half_t*)table;
     half_t* y = (half_t*)out;
     if (code_bytes == 1) {
-        hipLaunchKernelGGL(board_embedding_kernel<uint8_t>, dim3(B), dim3(256), 0, s, (const uint8_t*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+        hipLaunchKernelGGL(board_embedding_kernel<uint8_t>, dim3(grid), dim3(THREADS), 0, s, (const uint8_t*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
     } else if (code_bytes == 4) {
-        hipLaunchKernelGGL(board_embedding_kernel<int>, dim3(B), dim3(256), 0, s, (const int*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+        hipLaunchKernelGGL(board_embedding_kernel<int>, dim3(grid), dim3(THREADS), 0, s, (const int*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
     } else {
-        hipLaunchKernelGGL(board_embedding_kernel<long long>, dim3(B), dim3(256), 0, s, (const long long*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
+        hipLaunchKernelGGL(board_embedding_kernel<long long>, dim3(grid), dim3(THREADS), 0, s, (const long long*)boards, r, j, o, e, p, t, y, T, D, embed_rows, table_rows, codes);
     }
     return launch_status();
 }

@@ -1,4 +1,4 @@
-// The policy head's move logits of B positions, from the final norm's rows, one workgroup a position.
+// The policy head's move logits of B positions, from the final norm's rows.
 // Computes what model/fused_blocks.py:863-872 (the heads without fused ends) computes after its `a` matmul:
 //   narrow[t][c] = x[t] . W[c] + w_bias[c]                          c < NN: s, the promotion logits, board_down's
 //   logits[i][j] = (a[i] + a_bias) . x[j] + narrow[i][0]             i, j < 64, the squares
@@ -8,11 +8,14 @@
 // products in f32 (torch's F.linear and bmm); here they are f32 MFMAs (v_mfma_f32_32x32x2_f32: exact products,
 // f32 sums), so the results agree with it to f32 rounding, not to the bit.
 //
-// Four wavefronts: each takes a 32 x 32 quadrant of the logits, and wavefronts 0-2 a block of 32 token rows of the
-// narrow products (all NN <= 32 columns). A step covers 8 of D: lane l (row l % 32, half h = l / 32) loads 4
-// consecutive values k0 + 4h .. + 3 of its row of each operand and feeds them to 4 MFMAs, value m to MFMA m, so
-// that in MFMA m both operands' k-halves stand for k0 + m and k0 + 4 + m; eight steps' loads go out together. The
-// quadrants and the narrow rows meet in LDS for the gather of the 1,968 moves.
+// Two launches. The first takes one 32 x 32 block of products a workgroup: the 4 quadrants of the logits and the 3 blocks of
+// 32 token rows of the narrow products (all NN <= 32 columns), 7 workgroups a position, so that a batch of few positions
+// still spreads over the chip. Its wavefronts split D in up to 4 parts, whose partial blocks meet in LDS and are added in
+// part order. A step covers 8 of D: lane l (row l % 32, half h = l / 32) loads 4 consecutive values k0 + 4h .. + 3 of its
+// row of each operand and feeds them to 4 MFMAs, value m to MFMA m, so that in MFMA m both operands' k-halves stand for
+// k0 + m and k0 + 4 + m; eight steps' loads go out together. The blocks go to a workspace of the caller's, 7,168 floats a
+// position (the 64 x 64 logits, then 96 x 32 narrow products). The second launch, a workgroup a position, adds each
+// square's narrow column 0, gathers the 1,968 moves with their promotion logits, and writes board_down's inputs.
 #include "chess_common.h"
 
 #include <mutex>
@@ -22,8 +25,6 @@ namespace {
 constexpr int SQUARES = 64;
 constexpr int MAX_NARROW = 32;
 constexpr int MAX_TOKENS = 96;                 // three blocks of 32 token rows
-constexpr int LOGIT_STRIDE = SQUARES + 1;
-constexpr int NARROW_STRIDE = MAX_NARROW + 1;
 constexpr int THREADS = 256;
 
 typedef float v16f __attribute__((ext_vector_type(16)));
@@ -33,18 +34,18 @@ DEVICE v16f mfma_f32(float a, float b, v16f c) { return __builtin_amdgcn_mfma_f3
 // nn.GELU's exact form, 0.5 v (1 + erf(v / sqrt 2)), with the device library's erf
 DEVICE float gelu(float v) { return 0.5f * v * (1.0f + erff(v * 0.70710678118654752f)); }
 
-// the 32 x 32 block sum_k A[row0 + i][k] * X[col0 + j][k] over k < D: A's rows f32 (a_bias added when BIAS), X's fp16;
-// rows past a_rows and columns past x_rows read the last one (never kept). Lane l holds, in register 4q + r,
-// the sum for A row 8q + 4(l / 32) + r and X row l % 32. D is a multiple of 64: eight steps a turn, their loads
-// issued before their MFMAs, so that a turn's loads are in flight together.
+// the 32 x 32 block sum_k A[row0 + i][k] * X[col0 + j][k] over k < length, rows stride elements apart: A's rows f32 (a_bias
+// added when BIAS), X's fp16; rows past a_rows and columns past x_rows read the last one (never kept). Lane l holds, in
+// register 4q + r, the sum for A row 8q + 4(l / 32) + r and X row l % 32. length is a multiple of 64: eight steps a turn,
+// their loads issued before their MFMAs, so that a turn's loads are in flight together.
 template <bool BIAS>
-DEVICE v16f block_products(const float* A, int a_rows, const float* a_bias, const half_t* X, int x_rows, int D, int lane) {
+DEVICE v16f block_products(const float* A, int a_rows, const float* a_bias, const half_t* X, int x_rows, int length, int stride, int lane) {
     constexpr int TURN = 8;   // steps of 8 a turn
     const int r32 = lane & 31, h = lane >> 5;
-    const float* a_row = A + (size_t)min(r32, a_rows - 1) * D + 4 * h;
-    const half_t* x_row = X + (size_t)min(r32, x_rows - 1) * D + 4 * h;
+    const float* a_row = A + (size_t)min(r32, a_rows - 1) * stride + 4 * h;
+    const half_t* x_row = X + (size_t)min(r32, x_rows - 1) * stride + 4 * h;
     v16f acc = {};
-    for (int turn = 0; turn < D; turn += 8 * TURN) {
+    for (int turn = 0; turn < length; turn += 8 * TURN) {
         float4 av[TURN];
         v4h xv[TURN];
 #pragma unroll
@@ -68,61 +69,73 @@ DEVICE v16f block_products(const float* A, int a_rows, const float* a_bias, cons
     return acc;
 }
 
-__global__ __launch_bounds__(THREADS) void move_logits_kernel(
+constexpr int BLOCKS_A_POSITION = 4 + MAX_TOKENS / 32;
+constexpr int WORKSPACE_FLOATS = SQUARES * SQUARES + MAX_TOKENS * MAX_NARROW;   // a position's
+
+__global__ __launch_bounds__(THREADS) void head_blocks_kernel(
     const half_t* __restrict__ x, const float* __restrict__ a, const float* __restrict__ a_bias, const float* __restrict__ w,
-    const float* __restrict__ w_bias, const int* __restrict__ cells, const int* __restrict__ promotions, float* __restrict__ out,
-    float* __restrict__ down, int T, int D, int NN, int down_first, int moves, int out_stride, int activate)
+    const float* __restrict__ w_bias, float* __restrict__ workspace, int T, int D, int NN, int parts)
 {
-    __shared__ float logits[SQUARES * LOGIT_STRIDE];
-    __shared__ float narrow[MAX_TOKENS * NARROW_STRIDE];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const size_t b = blockIdx.x;
+    __shared__ float partial[4][32 * 32];
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int block = blockIdx.x;
+    const size_t b = blockIdx.y;
     const half_t* xb = x + b * T * D;
     const int r32 = lane & 31, h = lane >> 5;
-
-    // the wavefront's quadrant of a . x^T: rows i0.. of a (the from side), columns j0.. of x (the to side)
-    const int i0 = (wave >> 1) * 32, j0 = (wave & 1) * 32;
-    const v16f quadrant = block_products<true>(a + (b * T + i0) * D, 32, a_bias, xb + (size_t)j0 * D, 32, D, lane);
-
-    // narrow[t][c] for the wavefront's 32 token rows: W's rows (columns c) as the first operand, x's as the second
-    if (wave < 3) {
-        const int t0 = wave * 32;
-        if (t0 < T) {
-            const v16f products = block_products<false>(w, NN, nullptr, xb + (size_t)t0 * D, T - t0, D, lane);
+    const int t0 = (block - 4) * 32;
+    if (block >= 4 && t0 >= T) return;   // the whole workgroup: a narrow block past the tokens
+    const int part = D / parts, k0 = wave * part;
+    if (wave < parts) {
+        // quadrant: rows i0.. of a (the from side), columns j0.. of x (the to side); narrow: W's rows (columns c) and x's
+        // token rows t0..
+        const int i0 = (block >> 1) * 32, j0 = (block & 1) * 32;
+        const v16f products = block < 4
+            ? block_products<true>(a + (b * T + i0) * D + k0, 32, a_bias + k0, xb + (size_t)j0 * D + k0, 32, part, D, lane)
+            : block_products<false>(w + k0, NN, nullptr, xb + (size_t)t0 * D + k0, T - t0, part, D, lane);
 #pragma unroll
-            for (int q = 0; q < 4; q++)
+        for (int q = 0; q < 4; q++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int c = 8 * q + 4 * h + r, t = t0 + r32;
-                    if (c < NN && t < T) narrow[t * NARROW_STRIDE + c] = products[4 * q + r] + w_bias[c];
-                }
-        }
+            for (int r = 0; r < 4; r++) partial[wave][(8 * q + 4 * h + r) * 32 + r32] = products[4 * q + r];
     }
     __syncthreads();
-
-    // logits = the quadrant + s[i] (the from square's narrow column 0)
+    float* out = workspace + b * WORKSPACE_FLOATS;
 #pragma unroll
-    for (int q = 0; q < 4; q++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int i = i0 + 8 * q + 4 * h + r, j = j0 + r32;
-            logits[i * LOGIT_STRIDE + j] = quadrant[4 * q + r] + narrow[i * NARROW_STRIDE];
+    for (int e = tid; e < 32 * 32; e += THREADS) {
+        float sum = partial[0][e];
+        for (int p = 1; p < parts; p++) sum = sum + partial[p][e];
+        const int row = e / 32, column = e % 32;   // row of the first operand, column of the second
+        if (block < 4) {
+            out[((block >> 1) * 32 + row) * SQUARES + (block & 1) * 32 + column] = sum;
+        } else if (row < NN && t0 + column < T) {
+            out[SQUARES * SQUARES + (t0 + column) * MAX_NARROW + row] = sum + w_bias[row];
         }
-    __syncthreads();
+    }
+}
 
+__global__ __launch_bounds__(THREADS) void head_gather_kernel(
+    const float* __restrict__ workspace, const int* __restrict__ cells, const int* __restrict__ promotions, float* __restrict__ out,
+    float* __restrict__ down, int T, int NN, int down_first, int moves, int out_stride, int activate)
+{
+    const int tid = threadIdx.x;
+    const size_t b = blockIdx.x;
+    const float* logits = workspace + b * WORKSPACE_FLOATS;
+    const float* narrow = logits + SQUARES * SQUARES;
     // the moves: cells[m] = from * 64 + to; promotions[m] = to' * 32 + column of its promotion logit, or -1 (the places
-    // are masked into the tiles, so that no table entry reads outside them)
+    // are masked into the blocks, so that no table entry reads outside them); logits = the quadrant + s[from] (the from
+    // square's narrow column 0)
     float* out_b = out + b * out_stride;
+#pragma unroll 4
     for (int m = tid; m < moves; m += THREADS) {
-        const int cell = cells[m], promotion = promotions[m];
-        float value = logits[((cell >> 6) & 63) * LOGIT_STRIDE + (cell & 63)];
-        if (promotion >= 0) value = value + narrow[((promotion >> 5) & 63) * NARROW_STRIDE + (promotion & 31)];
+        const int cell = cells[m], promotion = promotions[m], from = (cell >> 6) & 63;
+        float value = logits[from * SQUARES + (cell & 63)] + narrow[from * MAX_NARROW];
+        if (promotion >= 0) value = value + narrow[((promotion >> 5) & 63) * MAX_NARROW + (promotion & 31)];
         out_b[m] = value;
     }
     const int width = NN - down_first;
     float* down_b = down + b * T * width;
+#pragma unroll 4
     for (int e = tid; e < T * width; e += THREADS) {
-        const float value = narrow[(e / width) * NARROW_STRIDE + down_first + e % width];
+        const float value = narrow[(e / width) * MAX_NARROW + down_first + e % width];
         down_b[e] = activate ? gelu(value) : value;
     }
 }
@@ -153,6 +166,7 @@ __global__ __launch_bounds__(THREADS) void value_hidden_kernel(const float* __re
     const float* a_row = c + (size_t)min(p0 + row, B - 1) * K + 4 * group;
     const float* b_row = weight + (size_t)(u0 + row) * K + 4 * group;
     v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll 6
     for (int chunk = wave; chunk < K / VALUE_CHUNK; chunk += 4) {
         const float4 a4 = *reinterpret_cast<const float4*>(a_row + chunk * VALUE_CHUNK);
         const float4 b4 = *reinterpret_cast<const float4*>(b_row + chunk * VALUE_CHUNK);
@@ -169,31 +183,38 @@ __global__ __launch_bounds__(THREADS) void value_hidden_kernel(const float* __re
     if (p0 + position < B) hidden[(size_t)(p0 + position) * H + u0 + unit] = gelu(sum + bias[u0 + unit]);
 }
 
-// The second layer, the softmax and the expected score, a wavefront a position: lane l takes bins l and l + 64 (their
-// W2 rows read 16 bytes at a time, the position's hidden row uniform across the wavefront), f32 fma along the units in
-// order; the maximum, the exponentials' sum and the centres' weighted sum are wavefront trees.
+// The second layer, the softmax and the expected score, a workgroup a position: thread t takes bin t % 128 over half t / 128
+// of the units (its W2 row read 16 bytes at a time, the position's hidden row uniform across each wavefront), f32 fma along
+// its units in order; the halves meet in LDS as first + second, then wavefront 0 holds bins l and l + 64 in lane l and takes
+// the maximum, the exponentials' sum and the centres' weighted sum as wavefront trees. A position's chain of dependent
+// loads is a quarter of one wavefront's walk over all the units, and a batch of few positions still spreads over the chip.
+constexpr int SCORE_PARTS = THREADS / MAX_BINS;
+
 __global__ __launch_bounds__(THREADS) void value_score_kernel(const float* __restrict__ hidden, const float* __restrict__ weight,
                                                               const float* __restrict__ bias, const float* __restrict__ centres,
                                                               float* __restrict__ logits, float* __restrict__ rows, int B, int H, int bins,
                                                               int row_stride, int score_column)
 {
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int b = blockIdx.x * 4 + wave;
-    if (b >= B) return;   // the whole wavefront: this kernel has no barriers
-    const float* h = hidden + (size_t)b * H;
-    const int v0 = lane, v1 = lane + 64;
-    const float* w0 = weight + (size_t)min(v0, bins - 1) * H;
-    const float* w1 = weight + (size_t)min(v1, bins - 1) * H;
-    float s0 = 0.0f, s1 = 0.0f;
-    for (int k = 0; k < H; k += 4) {
+    __shared__ float partial[SCORE_PARTS][MAX_BINS];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int b = blockIdx.x;
+    const int v = tid % MAX_BINS, part = tid / MAX_BINS, units = H / SCORE_PARTS;
+    const float* h = hidden + (size_t)b * H + part * units;
+    const float* wv = weight + (size_t)min(v, bins - 1) * H + part * units;
+    float sum = 0.0f;
+#pragma unroll 8
+    for (int k = 0; k < units; k += 4) {
         const float4 x = *reinterpret_cast<const float4*>(h + k);
-        const float4 a = *reinterpret_cast<const float4*>(w0 + k);
-        const float4 d = *reinterpret_cast<const float4*>(w1 + k);
-        s0 = __builtin_fmaf(x.x, a.x, s0); s0 = __builtin_fmaf(x.y, a.y, s0); s0 = __builtin_fmaf(x.z, a.z, s0); s0 = __builtin_fmaf(x.w, a.w, s0);
-        s1 = __builtin_fmaf(x.x, d.x, s1); s1 = __builtin_fmaf(x.y, d.y, s1); s1 = __builtin_fmaf(x.z, d.z, s1); s1 = __builtin_fmaf(x.w, d.w, s1);
+        const float4 a = *reinterpret_cast<const float4*>(wv + k);
+        sum = __builtin_fmaf(x.x, a.x, sum); sum = __builtin_fmaf(x.y, a.y, sum); sum = __builtin_fmaf(x.z, a.z, sum); sum = __builtin_fmaf(x.w, a.w, sum);
     }
+    partial[part][v] = sum;
+    __syncthreads();
+    if (tid >= 64) return;   // wavefronts 1-3: nothing waits for them past the barrier
+    const int v0 = lane, v1 = lane + 64;
     const bool in0 = v0 < bins, in1 = v1 < bins;
-    const float l0 = in0 ? s0 + bias[v0] : -__builtin_inff(), l1 = in1 ? s1 + bias[v1] : -__builtin_inff();
+    const float l0 = in0 ? (partial[0][v0] + partial[1][v0]) + bias[v0] : -__builtin_inff();
+    const float l1 = in1 ? (partial[0][v1] + partial[1][v1]) + bias[v1] : -__builtin_inff();
     const float top = wave_max(fmaxf(l0, l1));
     const float e0 = in0 ? expf(l0 - top) : 0.0f, e1 = in1 ? expf(l1 - top) : 0.0f;
     const float total = wave_sum(e0 + e1);
@@ -211,7 +232,7 @@ int value_head(const void* c, const void* hidden_weight, const void* hidden_bias
     hipLaunchKernelGGL(value_hidden_kernel, dim3((B + VALUE_TILE - 1) / VALUE_TILE, H / VALUE_TILE), dim3(THREADS), 0, stream,
                        (const float*)c, (const float*)hidden_weight, (const float*)hidden_bias, hidden, B, K, H);
     if (int status = launch_status()) return status;
-    hipLaunchKernelGGL(value_score_kernel, dim3((B + 3) / 4), dim3(THREADS), 0, stream, (const float*)hidden, (const float*)out_weight,
+    hipLaunchKernelGGL(value_score_kernel, dim3(B), dim3(THREADS), 0, stream, (const float*)hidden, (const float*)out_weight,
                        (const float*)out_bias, (const float*)centres, (float*)value_logits, (float*)rows, B, H, bins, row_stride, score_column);
     return launch_status();
 }
@@ -219,7 +240,7 @@ int value_head(const void* c, const void* hidden_weight, const void* hidden_bias
 int check_value_head(const void* c, const void* hidden_weight, const void* hidden_bias, const void* out_weight, const void* out_bias,
                      const void* centres, const void* rows, int B, int K, int H, int bins, int row_stride, int score_column)
 {
-    if (B < 0 || K <= 0 || K % VALUE_CHUNK != 0 || H <= 0 || H % VALUE_TILE != 0 || bins < 1 || bins > MAX_BINS)
+    if (B < 0 || K <= 0 || K % VALUE_CHUNK != 0 || H <= 0 || H % VALUE_TILE != 0 || H % (4 * SCORE_PARTS) != 0 || bins < 1 || bins > MAX_BINS)
         return chess_fail(CHESS_UNSUPPORTED, "value_head takes inputs and units a multiple of %d and at most %d bins, not %d, %d and %d",
                           VALUE_TILE, MAX_BINS, K, H, bins);
     if (row_stride <= 0 || score_column < 0 || score_column >= row_stride)
@@ -234,8 +255,8 @@ int check_value_head(const void* c, const void* hidden_weight, const void* hidde
 }  // namespace
 
 extern "C" int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
-                                 const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves,
-                                 int out_stride, int activate, void* stream)
+                                 const void* promotions, void* out, void* down, void* workspace, long long workspace_bytes, int B, int T, int D,
+                                 int NN, int down_first, int moves, int out_stride, int activate, void* stream)
 {
     if (B < 0 || T < SQUARES || T > MAX_TOKENS || D <= 0 || D % 64 != 0)
         return chess_fail(CHESS_UNSUPPORTED, "move_logits takes %d to %d tokens of a width that is a multiple of 64, not %d x %d", SQUARES, MAX_TOKENS,
@@ -245,12 +266,21 @@ extern "C" int chess_move_logits(const void* x, const void* a, const void* a_bia
                           MAX_NARROW, down_first, moves, out_stride);
     if (!x || !a || !a_bias || !w || !w_bias || !cells || !promotions || !out || !down)
         return chess_fail(CHESS_INVALID_SHAPE, "move_logits: a required pointer is null");
+    if (!workspace || workspace_bytes < (long long)B * WORKSPACE_FLOATS * (long long)sizeof(float))
+        return chess_fail(CHESS_INVALID_SHAPE, "move_logits' workspace holds %d floats a position, %lld bytes, not %lld", WORKSPACE_FLOATS,
+                          (long long)B * WORKSPACE_FLOATS * 4LL, workspace_bytes);
     if (!aligned16(x) || !aligned16(a) || !aligned16(a_bias) || !aligned16(w))
         return chess_fail(CHESS_MISALIGNED, "move_logits reads x, a, a_bias and W 8 and 16 bytes a lane");
     if (B == 0) return CHESS_OK;
-    hipLaunchKernelGGL(move_logits_kernel, dim3(B), dim3(THREADS), 0, (hipStream_t)stream, (const half_t*)x, (const float*)a,
-                       (const float*)a_bias, (const float*)w, (const float*)w_bias, (const int*)cells, (const int*)promotions, (float*)out,
-                       (float*)down, T, D, NN, down_first, moves, out_stride, activate);
+    // D split in the most parts (at most 4, one a wavefront) of a multiple of 64 each
+    int parts = 4;
+    while (D % (64 * parts) != 0) parts--;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(head_blocks_kernel, dim3(BLOCKS_A_POSITION, B), dim3(THREADS), 0, s, (const half_t*)x, (const float*)a,
+                       (const float*)a_bias, (const float*)w, (const float*)w_bias, (float*)workspace, T, D, NN, parts);
+    if (int status = launch_status()) return status;
+    hipLaunchKernelGGL(head_gather_kernel, dim3(B), dim3(THREADS), 0, s, (const float*)workspace, (const int*)cells, (const int*)promotions,
+                       (float*)out, (float*)down, T, NN, down_first, moves, out_stride, activate);
     return launch_status();
 }
 

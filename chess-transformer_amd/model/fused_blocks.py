@@ -359,15 +359,20 @@ def _check_head_operands(x, a, a_bias, narrow_weight, narrow_bias, cells, promot
         raise ValueError(f"{what}: a cell and a promotion place for every move")
 
 
+# floats a position of chess_move_logits' workspace: the 64 x 64 logits, then 96 tokens x 32 narrow products
+MOVE_LOGITS_WORKSPACE = NUM_SQUARES * NUM_SQUARES + 96 * 32
+
+
 def _launch_move_logits(x, a, a_bias, narrow_weight, narrow_bias, cells, promotions, down_first, out, out_stride, activate) -> torch.Tensor:
     B, T, D = x.shape
     library = library_for(x.device)
     x, a, a_bias, narrow_weight = aligned(x), aligned(a), aligned(a_bias), aligned(narrow_weight)
     narrow = narrow_weight.shape[0]
     down = torch.empty(B, T, narrow - down_first, device=x.device, dtype=torch.float32)
+    workspace = torch.empty(B, MOVE_LOGITS_WORKSPACE, device=x.device, dtype=torch.float32)
     code = library.chess_move_logits(pointer(x), pointer(a), pointer(a_bias), pointer(narrow_weight), pointer(narrow_bias.contiguous()),
-                                     pointer(cells.contiguous()), pointer(promotions.contiguous()), pointer(out), pointer(down), B, T, D, narrow,
-                                     down_first, cells.numel(), out_stride, int(activate), stream_of(x.device))
+                                     pointer(cells.contiguous()), pointer(promotions.contiguous()), pointer(out), pointer(down), pointer(workspace),
+                                     workspace.numel() * 4, B, T, D, narrow, down_first, cells.numel(), out_stride, int(activate), stream_of(x.device))
     check(code, "move_logits")
     return down
 

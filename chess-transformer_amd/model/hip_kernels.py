@@ -30,7 +30,7 @@ SIGNATURES = {
     "chess_template_attention": [_pointer] * 5 + [_int] * 8 + [_float, _float, _pointer],
     "chess_linear": [_pointer] * 8 + [_int] * 6 + [_pointer],
     "chess_board_embedding": [_pointer, _int] + [_pointer] * 7 + [_int] * 12 + [_pointer],
-    "chess_move_logits": [_pointer] * 9 + [_int] * 8 + [_pointer],
+    "chess_move_logits": [_pointer] * 10 + [ctypes.c_longlong] + [_int] * 8 + [_pointer],
     "chess_value_head": [_pointer] * 9 + [ctypes.c_longlong] + [_int] * 6 + [_pointer],
     "chess_value_head_no_alloc": [_pointer] * 8 + [_int] * 6 + [_pointer],
     "chess_lean_answers": [_pointer] * 3 + [_int] * 5 + [_pointer],

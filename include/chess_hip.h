@@ -97,11 +97,12 @@ int chess_board_embedding(const void* boards, int code_bytes, const void* rays, 
  * out[b * out_stride + m] f32 = ((a[from] + a_bias) . x[to]) + narrow[from][0] (+ narrow[to'][column]), m < moves
  * (out_stride = moves + 1 writes the answer rows' logits in place); down[B, T, NN - down_first] f32 =
  * narrow[t][down_first..NN), through nn.GELU when activate (board_down_project's activation, the value head's input).
- * 64 <= T <= 96, D % 64 == 0, NN <= 32. Replaces the torch ops of :866-871 (the f32 linear, the transposed bmm, the
- * gathers and the promotion sum). */
+ * 64 <= T <= 96, D % 64 == 0, NN <= 32. The products go through workspace (at least B * 7,168 * 4 bytes: a position's 64 x 64
+ * logits and 96 x 32 narrow products), which the call allocates nothing for. Replaces the torch ops of :866-871 (the f32
+ * linear, the transposed bmm, the gathers and the promotion sum). */
 int chess_move_logits(const void* x, const void* a, const void* a_bias, const void* w, const void* w_bias, const void* cells,
-                      const void* promotions, void* out, void* down, int B, int T, int D, int NN, int down_first, int moves, int out_stride,
-                      int activate, void* stream);
+                      const void* promotions, void* out, void* down, void* workspace, long long workspace_bytes, int B, int T, int D, int NN,
+                      int down_first, int moves, int out_stride, int activate, void* stream);
 
 /* The value head of B positions (the eval head after board_down_project, model/model.py:200-201, and the expected score,
  * :37-41; the reference's fused head_value_tile / head_value_kernel, model/fused_blocks.py:649-728): from c[B, K] f32,

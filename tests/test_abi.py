@@ -76,13 +76,16 @@ def test_refused_shapes_come_back_as_codes(library):
     assert library.chess_template_attention(16, 8, 16, 16, 16, 1, 70, 8, 8, 64, 64, 8, 1, 1e-5, 0.125, None) == hip_kernels.MISALIGNED
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
-    moves = lambda *shape, stride=1969: library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, *shape, stride, 1, None)
+    moves = lambda *shape, stride=1969, workspace=16, size=1 << 30: library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, workspace, size,
+                                                                                               *shape, stride, 1, None)
     assert moves(2, 63, 512, 21, 5, 1968) == hip_kernels.UNSUPPORTED      # fewer tokens than squares
     assert moves(2, 70, 500, 21, 5, 1968) == hip_kernels.UNSUPPORTED      # width not a multiple of 8
     assert moves(2, 70, 512, 33, 5, 1968) == hip_kernels.INVALID_SHAPE    # more narrow columns than a block
     assert moves(2, 70, 512, 21, 0, 1968) == hip_kernels.INVALID_SHAPE    # board_down's inputs from column 0
     assert moves(2, 70, 512, 21, 5, 1968, stride=1967) == hip_kernels.INVALID_SHAPE   # rows narrower than the moves
-    assert library.chess_move_logits(MISALIGNED, 16, 16, 16, 16, 16, 16, 16, 16, 2, 70, 512, 21, 5, 1968, 1968, 0, None) == hip_kernels.MISALIGNED
+    assert moves(2, 70, 512, 21, 5, 1968, workspace=None) == hip_kernels.INVALID_SHAPE          # no workspace
+    assert moves(2, 70, 512, 21, 5, 1968, size=2 * 7168 * 4 - 1) == hip_kernels.INVALID_SHAPE  # a workspace too small
+    assert library.chess_move_logits(MISALIGNED, 16, 16, 16, 16, 16, 16, 16, 16, 16, 1 << 20, 2, 70, 512, 21, 5, 1968, 1968, 0, None) == hip_kernels.MISALIGNED
     # the value head: widths a multiple of 16, at most 128 bins, the score inside the row, a workspace for the hidden layer
     value = lambda B, K, H, bins, stride=1969, column=1968, workspace=16, size=1 << 20: library.chess_value_head(
         16, 16, 16, 16, 16, 16, None, 16, workspace, size, B, K, H, bins, stride, column, None)
@@ -104,7 +107,7 @@ def test_refused_shapes_come_back_as_codes(library):
 def test_empty_batches_launch_nothing(library):
     assert library.chess_norm_quant(16, None, None, None, 16, None, 16, 16, 0, 64, 1e-5, None) == 0
     assert library.chess_rms_norm(16, None, None, None, 16, None, 16, 0, 64, 1e-5, None) == 0
-    assert library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, 0, 70, 512, 21, 5, 1968, 1969, 1, None) == 0
+    assert library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, 16, 0, 0, 70, 512, 21, 5, 1968, 1969, 1, None) == 0
     assert library.chess_value_head(16, 16, 16, 16, 16, 16, None, 16, 16, 0, 0, 1120, 512, 128, 1969, 1968, None) == 0
     assert library.chess_lean_answers(16, 16, 16, 0, 1969, 508, 70, 219, None) == 0
     assert library.chess_int8_linear(16, 16, 16, 16, None, None, None, None, None, 16, 0, 8, 64, 0, 0, 0, None) == 0
