@@ -74,12 +74,17 @@ constexpr int WORKSPACE_FLOATS = SQUARES * SQUARES + MAX_TOKENS * MAX_NARROW;   
 
 __global__ __launch_bounds__(THREADS) void head_blocks_kernel(
     const half_t* __restrict__ x, const float* __restrict__ a, const float* __restrict__ a_bias, const float* __restrict__ w,
-    const float* __restrict__ w_bias, float* __restrict__ workspace, int T, int D, int NN, int parts)
+    const float* __restrict__ w_bias, float* __restrict__ workspace, int B, int T, int D, int NN, int parts)
 {
     __shared__ float partial[4][32 * 32];
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int block = blockIdx.x;
-    const size_t b = blockIdx.y;
+    // The workgroups go to the 8 XCDs in turn, each with its own L2: a position's 7 blocks run on one XCD (positions
+    // x, x + 8, ... on XCD x), so that its rows of a and x come from that L2 after the first read.
+    constexpr int XCDS = 8;
+    const int xcd = blockIdx.x % XCDS, on_xcd = blockIdx.x / XCDS;
+    const int block = on_xcd % BLOCKS_A_POSITION;
+    const size_t b = (size_t)(on_xcd / BLOCKS_A_POSITION) * XCDS + xcd;
+    if (b >= (size_t)B) return;   // the whole workgroup: the launch rounds the positions up to a multiple of 8
     const half_t* xb = x + b * T * D;
     const int r32 = lane & 31, h = lane >> 5;
     const int t0 = (block - 4) * 32;
@@ -276,8 +281,8 @@ extern "C" int chess_move_logits(const void* x, const void* a, const void* a_bia
     int parts = 4;
     while (D % (64 * parts) != 0) parts--;
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(head_blocks_kernel, dim3(BLOCKS_A_POSITION, B), dim3(THREADS), 0, s, (const half_t*)x, (const float*)a,
-                       (const float*)a_bias, (const float*)w, (const float*)w_bias, (float*)workspace, T, D, NN, parts);
+    hipLaunchKernelGGL(head_blocks_kernel, dim3(BLOCKS_A_POSITION * ((B + 7) / 8 * 8)), dim3(THREADS), 0, s, (const half_t*)x, (const float*)a,
+                       (const float*)a_bias, (const float*)w, (const float*)w_bias, (float*)workspace, B, T, D, NN, parts);
     if (int status = launch_status()) return status;
     hipLaunchKernelGGL(head_gather_kernel, dim3(B), dim3(THREADS), 0, s, (const float*)workspace, (const int*)cells, (const int*)promotions,
                        (float*)out, (float*)down, T, NN, down_first, moves, out_stride, activate);
