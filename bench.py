@@ -11,6 +11,7 @@ python bench.py --kernel-only      the dominant kernel and a plain copy alone, f
 python bench.py --pmc-summary DIR  reads those two runs' counter_collection.csv files and prints the HBM bytes per launch
 python bench.py --network-only     eager forwards of the network at --batch (no graph, no timing), for rocprofv3 --pmc runs
                                    whose counters are summarised per kernel by --counter-summary DIR
+python bench.py --trace-summary DIR  per-kernel durations of the graph replays in a rocprofv3 --kernel-trace run
 """
 from __future__ import annotations
 
@@ -336,8 +337,10 @@ def kernel_role(name: str) -> str:
             return "fp16 block gate_up"
         return {"3": "combine (fp16, bias + residual)", "1": "fp16 block projection", "2": "fp16 block down",
                 "6": "fp16 block down (mix)"}.get(epilogue, "fp16 gemm")
-    for key, role in (("norm_quant_kernel", "norm_quant"), ("rotate_quant", "rotate_quant"), ("template_attention", "template_attention"),
-                      ("board_embedding", "board_embedding"), ("move_logits", "move_logits"), ("value_hidden", "value_hidden"),
+    for key, role in (("norm_quant_kernelILi8ELi1ELb1ELb0", "rms_norm (fp16 block, final norm)"), ("norm_quant_kernelILi8ELi2ELb1ELb0", "rms_norm (fp16 block, final norm)"),
+                      ("norm_quant_kernel", "norm_quant"), ("rotate_quant", "rotate_quant"), ("template_attention", "template_attention"),
+                      ("board_embedding", "board_embedding"), ("head_blocks", "move logits: product blocks"), ("head_gather", "move logits: gather"),
+                      ("move_logits", "move_logits"), ("value_hidden", "value_hidden"),
                       ("value_score", "value_score"), ("copy", "copy")):
         if key in name:
             return role
@@ -383,6 +386,44 @@ def counter_summary(folder: Path) -> int:
                  ratio(mean.get("SQ_WAVE_CYCLES"), waves, 4, 0),
                  f"{mean['FETCH_SIZE']:,.0f}" if "FETCH_SIZE" in mean else "", f"{mean['WRITE_SIZE']:,.0f}" if "WRITE_SIZE" in mean else ""]
         print(f"| {role} | {dispatches} | " + " | ".join(cells) + " |")
+    return 0
+
+
+def trace_summary(folder: Path) -> int:
+    """Per kernel role, the average duration and the time a forward, over the graph replays in the rocprofv3 --kernel-trace
+    run under folder (its kernel_trace.csv): a forward starts at the input embedding's launch, and the replays are the
+    forwards that run without gaps (the eager forwards of the roofline timing have host gaps between their launches)."""
+    import csv
+    rows = []
+    for path in sorted(folder.rglob("*kernel_trace.csv")):
+        rows += list(csv.DictReader(path.open()))
+    rows.sort(key=lambda row: int(row["Start_Timestamp"]))
+    starts = [i for i, row in enumerate(rows) if kernel_role(row["Kernel_Name"]) == "board_embedding"] + [len(rows)]
+    forwards = []
+    for first, end in zip(starts, starts[1:]):
+        span = int(rows[end - 1]["End_Timestamp"]) - int(rows[first]["Start_Timestamp"])
+        busy = sum(int(row["End_Timestamp"]) - int(row["Start_Timestamp"]) for row in rows[first:end])
+        if busy >= 0.95 * span:
+            forwards.append(rows[first:end])
+    if not forwards:
+        print("no graph replays found")
+        return 1
+    durations: dict[str, list[float]] = {}
+    shapes: dict[str, str] = {}
+    for forward in forwards:
+        for row in forward:
+            role = kernel_role(row["Kernel_Name"])
+            durations.setdefault(role, []).append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) / 1e3)
+            shapes[role] = f"{int(row['Grid_Size_X']) // int(row['Workgroup_Size_X'])} x {row['Workgroup_Size_X']}"
+    spans = [(int(f[-1]["End_Timestamp"]) - int(f[0]["Start_Timestamp"])) / 1e3 for f in forwards]
+    total = sum(spans) / len(spans)
+    print(f"{len(forwards)} graph replays, {len(forwards[0])} launches and {total:,.1f} us a forward\n")
+    print("| kernel | workgroups x threads | launches a forward | average us | us a forward | share |")
+    print("|---|---|---|---|---|---|")
+    for role, values in sorted(durations.items(), key=lambda item: -sum(item[1])):
+        each = sum(values) / len(values)
+        per_forward = sum(values) / len(forwards)
+        print(f"| {role} | {shapes[role]} | {len(values) // len(forwards)} | {each:,.1f} | {per_forward:,.1f} | {per_forward / total:.1%} |")
     return 0
 
 
@@ -497,11 +538,14 @@ def main() -> int:
     parser.add_argument("--pmc-summary", type=Path, help="summarise the FETCH_SIZE / WRITE_SIZE runs under this folder")
     parser.add_argument("--network-only", action="store_true", help="eager forwards of the network at --batch, for counter runs")
     parser.add_argument("--counter-summary", type=Path, help="per-kernel table of the counter runs under this folder")
+    parser.add_argument("--trace-summary", type=Path, help="per-kernel table of the graph replays in the kernel trace under this folder")
     arguments = parser.parse_args()
     if arguments.pmc_summary:
         return pmc_summary(arguments.pmc_summary, arguments.batch)
     if arguments.counter_summary:
         return counter_summary(arguments.counter_summary)
+    if arguments.trace_summary:
+        return trace_summary(arguments.trace_summary)
     if arguments.gpus != 1:
         print(f"bench.py measures one GPU: every box here has one and nothing in this build uses a second (asked for {arguments.gpus})",
               file=sys.stderr)
