@@ -28,6 +28,7 @@
 namespace {
 
 constexpr int MAX_TEMPLATES = 8;
+constexpr long SPLIT_PAIRS = 4096;   // (position, key/value group) pairs from which a 65-80 token launch takes the split slab
 constexpr float LOG2E = 1.44269504f;
 
 typedef __fp16 h2 __attribute__((ext_vector_type(2)));
@@ -77,20 +78,38 @@ DEVICE float squares8(const v8h& v, float c) {
     return dot2(w.w, w.w, dot2(w.z, w.z, dot2(w.y, w.y, dot2(w.x, w.x, c))));
 }
 
+// a workgroup's threads: Layout::WAVES wavefronts
+template <int TILES, bool SPLIT> constexpr int attention_threads() { return 64 * (SPLIT ? 4 : TILES); }
+
 // TILES: key tiles of 16 the instantiation holds (T <= 16 TILES)
-template <int DQP, int DV, int TILES>
+template <int DQP, int DV, int TILES, bool SPLIT = false>
 struct Layout {
     static constexpr int STEPS = (TILES + 1) / 2;     // 32-key steps of P V
     static constexpr int KEYS = TILES * 16;           // keys (and queries) staged
-    static constexpr int VKEYS = STEPS * 32;          // value keys staged (P is zero past T)
     static constexpr int KC = DQP / 8, VC = DV / 8;   // 16-byte chunks a raw key (query) row, a raw value row
-    // LDS in bytes: two buffers of keys (raw as they land, normalised in place), two of raw values, then two buffers of
-    // raw queries and template coefficients
+    // value keys staged, whole DMA instructions of them (64 chunks): a half step of P V past them reads zeros
+    static constexpr int VKEYS = (KEYS * VC + 63) / 64 * 64 / VC;
+    // SPLIT (five tiles: 65 to 80 tokens, the network's 70): four wavefronts, one a slab of 16 square queries, and the
+    // slab of the tokens past the squares split over three of them by 32-key step of P V (its partial maxima, sums and
+    // outputs meet in LDS), so that a workgroup's wavefronts spread evenly over a compute unit's four SIMDs and two
+    // workgroups fit one. Else one wavefront a slab.
+    static constexpr bool META = SPLIT;
+    static_assert(!SPLIT || TILES == 5, "the split slab is the fifth");
+    static constexpr int WAVES = META ? 4 : TILES;
+    // With five tiles every slab's softmax sum and P V outputs are added by 32-key step, in step order, whichever
+    // wavefront holds them, so that both launches give a query the same bits.
+    static constexpr bool BY_STEP = TILES == 5;
+    static_assert(attention_threads<TILES, SPLIT>() == 64 * WAVES, "the launch bounds' threads");
+    // LDS in bytes: two buffers of keys (raw as they land, normalised in place), two of raw values, the partial results
+    // of the split slab, then two buffers of raw queries and template coefficients
     static constexpr int RAW_K_BYTES = KEYS * DQP * 2;   // a buffer's
     static constexpr int RAW_V_BYTES = VKEYS * DV * 2;   // a buffer's
     static constexpr int RAW_Q_BYTES = KEYS * DQP * 2;   // a head's
     static constexpr int COEF_BYTES = 64 * MAX_TEMPLATES * 2;   // a head's template coefficients, a square query a row
-    static constexpr int FIXED_BYTES = 2 * RAW_K_BYTES + 2 * RAW_V_BYTES;
+    static constexpr int META_PARTS = 3;                 // the split slab's 32-key steps, one a wavefront
+    static constexpr int META_OUT = 64 * (DV / 4);       // a part's outputs: a lane's DV / 16 fragments of 4 f32
+    static constexpr int META_BYTES = META ? META_PARTS * (2 * 16 + META_OUT) * 4 : 0;
+    static constexpr int FIXED_BYTES = 2 * RAW_K_BYTES + 2 * RAW_V_BYTES + META_BYTES;
     static int bytes(int per_kv) { return FIXED_BYTES + 2 * per_kv * (RAW_Q_BYTES + COEF_BYTES); }
 };
 
@@ -140,18 +159,22 @@ struct DmaPlan {
 // scratch reload would wait for the DMA in flight too); query widths of 128, and value widths of 128 past 96 tokens,
 // spill some. (Fewer registers for more workgroups a CU cost more instructions than they gain: the kernel is bound
 // by its VALU work.)
-template <int DQP, int DV, int TILES>
-__global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2))) void template_attention_kernel(
+template <int DQP, int DV, int TILES, bool SPLIT>
+__global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__((amdgpu_waves_per_eu(2))) void template_attention_kernel(
     const half_t* __restrict__ projected, const half_t* __restrict__ keyed, const half_t* __restrict__ q_gain,
     const half_t* __restrict__ k_gain, half_t* __restrict__ out, int T, int heads, int kv_heads, int dq, int templates_count,
     int groups_per_block, float eps, float scale)
 {
-    typedef Layout<DQP, DV, TILES> L;
-    constexpr int KC = L::KC, VC = L::VC, WAVES = TILES, THREADS = 64 * TILES, STEPS = L::STEPS, KEYS = L::KEYS;
+    typedef Layout<DQP, DV, TILES, SPLIT> L;
+    constexpr int KC = L::KC, VC = L::VC, WAVES = L::WAVES, THREADS = 64 * WAVES, STEPS = L::STEPS, KEYS = L::KEYS;
     extern __shared__ __align__(16) int8_t lds[];
     LDS_SPACE int8_t* raw_k = (LDS_SPACE int8_t*)lds;                        // [2][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_v = raw_k + 2 * L::RAW_K_BYTES;                    // [2][VKEYS * DV halves]
-    LDS_SPACE int8_t* raw_q = raw_v + 2 * L::RAW_V_BYTES;                    // [2][per_kv][KEYS * DQP halves]
+    // the split slab's parts: maxima [3][16], sums [3][16], outputs [3][64 lanes][DV / 4] (f32)
+    float* meta_max = (float*)(lds + 2 * L::RAW_K_BYTES + 2 * L::RAW_V_BYTES);
+    float* meta_sum = meta_max + L::META_PARTS * 16;
+    float* meta_out = meta_sum + L::META_PARTS * 16;
+    LDS_SPACE int8_t* raw_q = raw_v + 2 * L::RAW_V_BYTES + L::META_BYTES;    // [2][per_kv][KEYS * DQP halves]
     LDS_SPACE int8_t* raw_c = raw_q + 2 * (heads / kv_heads) * L::RAW_Q_BYTES;   // [2][per_kv][64][8 halves]
 
     const int tid = threadIdx.x, lane = tid & 63, slab = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -170,7 +193,7 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
 
     // the DMA plans: keys and queries share one (same rows, same chunks), values have their own
     DmaPlan<KEYS, KC, WAVES> key_plan;
-    DmaPlan<STEPS * 32, VC, WAVES> value_plan;
+    DmaPlan<L::VKEYS, VC, WAVES> value_plan;
     key_plan.plan(T - 1, width, slab, lane);
     value_plan.plan(T - 1, width, slab, lane);
     const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
@@ -222,8 +245,9 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             gains[ks][e] = d < dq ? (float)q_gain[min(d, dq - 1)] : 0.0f;
         }
     constexpr int PART_CHUNKS = KC / 4;
-    static_assert(KEYS * 4 == THREADS && KC % 4 == 0, "four threads a key");
-    const int scale_key = tid / 4, first_chunk = (tid % 4) * PART_CHUNKS;
+    constexpr int KEY_PASSES = (KEYS * 4 + THREADS - 1) / THREADS;   // the keys normalised THREADS / 4 at a time
+    static_assert(KC % 4 == 0, "four threads a key");
+    const int first_chunk = (tid % 4) * PART_CHUNKS;
     float key_gains[PART_CHUNKS][8];
 #pragma unroll
     for (int c = 0; c < PART_CHUNKS; c++)
@@ -252,7 +276,8 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
             for (int k = 0; k < O_ITEMS; k++) {
                 const int item = tid + k * THREADS, q = item / VC, c = item % VC;
-                if ((O_TOTAL % THREADS == 0 || item < O_TOTAL) && q < T) {
+                // the split slab's rows (past the squares) are written by its merge, not staged
+                if ((O_TOTAL % THREADS == 0 || item < O_TOTAL) && q < (L::META ? min(T, 64) : T)) {
                     const uint4 eight = lds_read16_settled(staged + raw_slot<KC>(q, c) * 16);
                     *reinterpret_cast<uint4*>(to + (size_t)q * (heads * DV) + c * 8) = eight;
                 }
@@ -277,7 +302,10 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
         // the keys normalised in place: k' = f16((k * (1 / sqrt(mean of squares + eps))) * k_gain) over the key's dq columns,
         // the four threads of a key adding their partial sums as (a + b) + (c + d). Past dq a raw key chunk holds another
         // head's columns: zeroed, as a zero query column would not cancel an infinite one.
-        {
+#pragma unroll
+        for (int pass = 0; pass < KEY_PASSES; pass++) {
+            const int scale_key = pass * (THREADS / 4) + tid / 4;
+            if (KEYS * 4 % THREADS != 0 && scale_key >= KEYS) break;   // a whole wavefront: the last pass's keys are 16 of them
             LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
             v8h raw[PART_CHUNKS];
             float squares = 0.0f;
@@ -390,16 +418,35 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
             top = fmaxf(top, __shfl_xor(top, 32, 64));
             float total = 0.0f;
             const float offset = -top * LOG2E;
+            if constexpr (L::BY_STEP) {
+                // each 32-key step's sum across the wavefront, then the steps' sums in order
 #pragma unroll
-            for (int kt = 0; kt < 2 * STEPS; kt++)
+                for (int st = 0; st < STEPS; st++) {
+                    float step_total = 0.0f;
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const float p = kt < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], LOG2E, offset)) : 0.0f;
-                    s[kt][r] = p;
-                    total += p;
+                    for (int kt = 2 * st; kt < 2 * st + 2; kt++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float p = kt < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], LOG2E, offset)) : 0.0f;
+                            s[kt][r] = p;
+                            step_total += p;
+                        }
+                    step_total += __shfl_xor(step_total, 16, 64);
+                    step_total += __shfl_xor(step_total, 32, 64);
+                    total = st == 0 ? step_total : total + step_total;
                 }
-            total += __shfl_xor(total, 16, 64);
-            total += __shfl_xor(total, 32, 64);
+            } else {
+#pragma unroll
+                for (int kt = 0; kt < 2 * STEPS; kt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float p = kt < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(s[kt][r], LOG2E, offset)) : 0.0f;
+                        s[kt][r] = p;
+                        total += p;
+                    }
+                total += __shfl_xor(total, 16, 64);
+                total += __shfl_xor(total, 32, 64);
+            }
             const float inverse_total = __builtin_amdgcn_rcpf(total);
 
             // O^T = V^T P^T over 32-key steps: position e of both operands is key 32 st + 16 (e / 4) + 4 quad + e % 4.
@@ -430,7 +477,8 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
                     halves[dt][0] = transposed_read<32 * st * ROW_BYTES>(value_base[dt]);
-                    halves[dt][1] = transposed_read<(32 * st + 16) * ROW_BYTES>(value_base[dt]);
+                    if constexpr (32 * st + 16 < L::VKEYS) halves[dt][1] = transposed_read<(32 * st + 16) * ROW_BYTES>(value_base[dt]);
+                    else halves[dt][1] = v2u{0, 0};   // keys past the staged rows: P is zero there
                 }
                 asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
@@ -438,7 +486,11 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                     asm volatile("" : "+v"(halves[dt][0]), "+v"(halves[dt][1]));
                     const v4h lo = __builtin_bit_cast(v4h, halves[dt][0]), hi = __builtin_bit_cast(v4h, halves[dt][1]);
                     const v8h vf = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                    o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+                    if constexpr (L::BY_STEP && st > 0) {
+                        o[dt] = o[dt] + __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, v4f{0, 0, 0, 0}, 0, 0, 0);
+                    } else {
+                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+                    }
                 }
             });
             if constexpr (STAGED) {
@@ -459,6 +511,117 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
                     *reinterpret_cast<v4h*>(to + dt * 16) = result;
                 }
             }
+
+            if constexpr (L::META) {
+                // The slab of queries 64..79 (the tokens past the squares: no template bias), split by 32-key step of
+                // P V: wavefronts 0, 1 and 3 take steps 0, 1 and 2 (key tiles 2p, 2p + 1), wavefront 2 adds their parts.
+                // Each part's maximum is exchanged first, so that every part's probabilities are f16(exp(s - the
+                // row's maximum)) as in the one-wavefront slab; the parts' sums and outputs are added in part order.
+                const int part = slab == 3 ? 2 : slab;   // wavefront 2: the merge
+                const int meta_query = 64 + col;
+                float ms[2][4];
+                if (slab != 2) {
+                    v8h mq[DQP / 32];
+                    float msquares = 0.0f;
+#pragma unroll
+                    for (int ks = 0; ks < DQP / 32; ks++) {
+                        const int c = ks * 4 + quad;
+                        mq[ks] = *reinterpret_cast<const LDS_SPACE v8h*>(queries + raw_slot<KC>(meta_query, c) * 16);
+                        if (c * 8 >= dq) mq[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
+                        msquares = squares8(mq[ks], msquares);
+                    }
+                    msquares += __shfl_xor(msquares, 16, 64);
+                    msquares += __shfl_xor(msquares, 32, 64);
+                    const float mq_inverse = 1.0f / __builtin_sqrtf(msquares / columns + eps);
+#pragma unroll
+                    for (int ks = 0; ks < DQP / 32; ks++)
+#pragma unroll
+                        for (int e = 0; e < 8; e++) mq[ks][e] = (half_t)(((float)mq[ks][e] * mq_inverse) * gains[ks][e]);
+                    float mtop = -__builtin_inff();
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; h2++) {
+                        const int kt = 2 * part + h2;
+                        if (kt >= TILES) {
+#pragma unroll
+                            for (int r = 0; r < 4; r++) ms[h2][r] = -__builtin_inff();
+                            continue;
+                        }
+                        v4f acc = v4f{0, 0, 0, 0};
+#pragma unroll
+                        for (int ks = 0; ks < DQP / 32; ks++) {
+                            const v8h kf = *reinterpret_cast<const LDS_SPACE v8h*>(keys + raw_slot<KC>(kt * 16 + col, ks * 4 + quad) * 16);
+                            acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, mq[ks], acc, 0, 0, 0);
+                        }
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float value = kt * 16 + quad * 4 + r >= T ? -__builtin_inff() : acc[r] * scale;
+                            ms[h2][r] = value;
+                            mtop = fmaxf(mtop, value);
+                        }
+                    }
+                    mtop = fmaxf(mtop, __shfl_xor(mtop, 16, 64));
+                    mtop = fmaxf(mtop, __shfl_xor(mtop, 32, 64));
+                    if (quad == 0) meta_max[part * 16 + col] = mtop;
+                }
+                lds_barrier();   // the parts' maxima are in place
+                if (slab != 2) {
+                    const float top_all = fmaxf(fmaxf(meta_max[col], meta_max[16 + col]), meta_max[32 + col]);
+                    const float moffset = -top_all * LOG2E;
+                    float mtotal = 0.0f;
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; h2++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++) {
+                            const float p = 2 * part + h2 < TILES ? __builtin_amdgcn_exp2f(__builtin_fmaf(ms[h2][r], LOG2E, moffset)) : 0.0f;
+                            ms[h2][r] = p;
+                            mtotal += p;
+                        }
+                    mtotal += __shfl_xor(mtotal, 16, 64);
+                    mtotal += __shfl_xor(mtotal, 32, 64);
+                    if (quad == 0) meta_sum[part * 16 + col] = mtotal;
+                    v8h pf;
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        pf[r] = (half_t)ms[0][r];
+                        pf[4 + r] = (half_t)ms[1][r];
+                    }
+                    constexpr int ROW_BYTES = VC * 16;
+                    const int lo_rows = 32 * part * ROW_BYTES, hi_rows = (32 * part + 16) * ROW_BYTES;
+                    const bool has_hi = 32 * part + 16 < L::VKEYS;
+                    v2u halves[DV / 16][2];
+#pragma unroll
+                    for (int dt = 0; dt < DV / 16; dt++) {
+                        halves[dt][0] = transposed_read<0>(value_base[dt] + lo_rows);
+                        halves[dt][1] = has_hi ? transposed_read<0>(value_base[dt] + hi_rows) : v2u{0, 0};
+                    }
+                    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+                    float* mine = meta_out + part * L::META_OUT + lane * (DV / 4);
+#pragma unroll
+                    for (int dt = 0; dt < DV / 16; dt++) {
+                        asm volatile("" : "+v"(halves[dt][0]), "+v"(halves[dt][1]));
+                        const v4h lo = __builtin_bit_cast(v4h, halves[dt][0]), hi = __builtin_bit_cast(v4h, halves[dt][1]);
+                        const v8h vf = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                        const v4f partial = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, v4f{0, 0, 0, 0}, 0, 0, 0);
+                        *reinterpret_cast<v4f*>(mine + dt * 4) = partial;
+                    }
+                }
+                lds_barrier();   // the parts' sums and outputs are in place
+                if (slab == 2 && meta_query < T) {
+                    const float mtotal = (meta_sum[col] + meta_sum[16 + col]) + meta_sum[32 + col];
+                    const float minverse = __builtin_amdgcn_rcpf(mtotal);
+                    half_t* to = out + (b * T + meta_query) * (heads * DV) + head * DV + quad * 4;
+#pragma unroll
+                    for (int dt = 0; dt < DV / 16; dt++) {
+                        const v4f p0 = *reinterpret_cast<const v4f*>(meta_out + lane * (DV / 4) + dt * 4);
+                        const v4f p1 = *reinterpret_cast<const v4f*>(meta_out + L::META_OUT + lane * (DV / 4) + dt * 4);
+                        const v4f p2 = *reinterpret_cast<const v4f*>(meta_out + 2 * L::META_OUT + lane * (DV / 4) + dt * 4);
+                        v4h result;
+#pragma unroll
+                        for (int r = 0; r < 4; r++) result[r] = (half_t)(((p0[r] + p1[r]) + p2[r]) * minverse);
+                        *reinterpret_cast<v4h*>(to + dt * 16) = result;
+                    }
+                }
+            }
         }
     }
     if constexpr (STAGED) {
@@ -468,20 +631,20 @@ __global__ __launch_bounds__(64 * TILES) __attribute__((amdgpu_waves_per_eu(2)))
     }
 }
 
-template <int DQP, int DV, int TILES>
+template <int DQP, int DV, int TILES, bool SPLIT = false>
 int launch(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
            int kv_heads, int dq, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
-    typedef Layout<DQP, DV, TILES> L;
+    typedef Layout<DQP, DV, TILES, SPLIT> L;
     const int bytes = L::bytes(heads / kv_heads);
     if (bytes > 160 * 1024)
         return chess_fail(CHESS_UNSUPPORTED, "template_attention would stage %d bytes of LDS for %d heads a key/value head", bytes, heads / kv_heads);
-    auto kernel = template_attention_kernel<DQP, DV, TILES>;
+    auto kernel = template_attention_kernel<DQP, DV, TILES, SPLIT>;
     if (bytes > 65536) {
         const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (allowed != hipSuccess) return (int)allowed;
     }
-    const dim3 grid((unsigned)((long)B * kv_heads / groups_per_block)), block(64 * TILES);   // TILES == ceil(T / 16): the caller picked it so
+    const dim3 grid((unsigned)((long)B * kv_heads / groups_per_block)), block(64 * L::WAVES);   // TILES == ceil(T / 16): the caller picked it so
     hipLaunchKernelGGL(kernel, grid, block, bytes, stream, (const half_t*)projected, (const half_t*)keyed, (const half_t*)q_gain,
                        (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale);
     return launch_status();
@@ -493,7 +656,15 @@ int by_tokens(const void* projected, const void* keyed, const void* q_gain, cons
 {
     switch ((T + 15) / 16) {
         case 4: return launch<DQP, DV, 4>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        case 5: return launch<DQP, DV, 5>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 5:
+            // four wavefronts a workgroup (the split slab) once the launch has pairs to keep two workgroups on each compute
+            // unit busy: at 70 tokens and 8 x 64 heads on an MI355X, each at its best run of pairs a workgroup, batch 1024
+            // in 117.5 against 122.0 us, batch 512 in 62.5 against 65.0; batch 256 36.5 against 36.2, batch 128 22.6
+            // against 21.5. Query and value widths up to 64: past them the split slab's registers spill.
+            if constexpr (DQP <= 64 && DV <= 64)
+                if ((long)B * kv_heads >= SPLIT_PAIRS)
+                    return launch<DQP, DV, 5, true>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+            return launch<DQP, DV, 5>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
         case 6: return launch<DQP, DV, 6>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
         case 7: return launch<DQP, DV, 7>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
         default: return launch<DQP, DV, 8>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);

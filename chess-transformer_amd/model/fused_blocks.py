@@ -33,9 +33,10 @@ LINEAR_F32_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
 # step (190 against 226 us at 71,680 rows)
 LINEAR_LONG_ROW_TILES = {"gfx950": [(4, 1), (math.inf, 13)]}
 LONG_ROW_BYTES = 2048
-# the workgroups an attention launch keeps while a workgroup takes as many (position, key/value group) pairs as it can:
-# a workgroup's start (its template registers and first loads) is paid once for its pairs
-ATTENTION_WORKGROUPS = 1024
+# from this many (position, key/value group) pairs a template_attention launch of 65 to 80 tokens, query and value widths
+# up to 64, splits the slab of the tokens past the squares over three wavefronts: workgroups of four wavefronts instead
+# of five (the kernel's SPLIT_PAIRS)
+ATTENTION_SPLIT_PAIRS = 4096
 
 
 #the first of [(the most rows a multiprocessor's share may be, tile), ...] that the share fits, the last taking any
@@ -55,12 +56,22 @@ def linear_tile(device: torch.device, M: int, accumulate_fp32: bool = False, row
     return tile_for(table.get(arch, table["gfx950"]), M, torch.cuda.get_device_properties(device).multi_processor_count)
 
 
-def groups_per_workgroup(positions: int, kv_heads: int, multiprocessors: int = 256) -> int:
-    """The most (position, key/value group) pairs a workgroup takes -- a divisor of all the launch's pairs -- while the launch keeps
-    ATTENTION_WORKGROUPS workgroups, or half as many as pairs, but at least one a compute unit; any choice gives the same bits.
-    Timed on an MI355X: batch 64 (512 pairs) runs fastest at 256 workgroups of 2 pairs, batch 16 at one pair a workgroup."""
+def attention_waves(positions: int, kv_heads: int, tokens: int, dq: int, dv: int) -> int:
+    """A template_attention workgroup's wavefronts: one a slab of 16 queries, or four for the split slab."""
+    tiles = (tokens + 15) // 16
+    split = tiles == 5 and dq <= 64 and dv <= 64 and positions * kv_heads >= ATTENTION_SPLIT_PAIRS
+    return 4 if split else tiles
+
+
+def groups_per_workgroup(positions: int, kv_heads: int, multiprocessors: int = 256, tokens: int = 70, dq: int = 64, dv: int = 64) -> int:
+    """The most (position, key/value group) pairs a workgroup takes -- a divisor of all the launch's pairs -- while the launch
+    keeps as many workgroups as the compute units hold at once (two wavefronts a SIMD, four SIMDs: one workgroup of five to
+    eight wavefronts, two of four), so that a workgroup's start (its template registers and first loads) is paid once for
+    its pairs; any choice gives the same bits. Timed on an MI355X at 70 tokens and 8 x 64 heads: batch 16 at one pair a
+    workgroup, batch 64 at 256 workgroups of 2 pairs (13.7 us), batch 1024 at 512 of 16 (117.5 us; 256 of 32 in 122.0
+    and 1,024 of 8 in 137.7 before the split slab)."""
     pairs = positions * kv_heads
-    workgroups = max(multiprocessors, min(ATTENTION_WORKGROUPS, pairs // 2))
+    workgroups = multiprocessors * max(1, 8 // attention_waves(positions, kv_heads, tokens, dq, dv))
     groups = max(1, pairs // workgroups)
     while pairs % groups:
         groups -= 1
@@ -82,7 +93,7 @@ def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, 
     projected = aligned(projected)
     keyed = keyed_templates(templates, templates_count)
     out = torch.empty(B, T, heads * dv, device=projected.device, dtype=torch.float16)
-    groups = groups_per_block or groups_per_workgroup(B, kv_heads, torch.cuda.get_device_properties(projected.device).multi_processor_count)
+    groups = groups_per_block or groups_per_workgroup(B, kv_heads, torch.cuda.get_device_properties(projected.device).multi_processor_count, T, dq, dv)
     code = library.chess_template_attention(pointer(projected), pointer(keyed), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()),
                                             pointer(out), B, T, heads, kv_heads, dq, dv, templates_count, groups, float(eps), 1 / math.sqrt(dq),
                                             stream_of(projected.device))

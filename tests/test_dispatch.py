@@ -20,20 +20,25 @@ def test_tile_for_takes_the_first_row_share_that_fits():
 
 @pytest.mark.parametrize("positions", [1, 3, 16, 64, 100, 256, 1024, 4096])
 @pytest.mark.parametrize("kv_heads", [8, 12])
-def test_attention_runs_divide_the_pairs_and_keep_the_chip_busy(positions, kv_heads):
+@pytest.mark.parametrize("tokens", [64, 70, 100])
+def test_attention_runs_divide_the_pairs_and_keep_the_chip_busy(positions, kv_heads, tokens):
     pairs = positions * kv_heads
-    groups = groups_per_workgroup(positions, kv_heads, 256)
+    groups = groups_per_workgroup(positions, kv_heads, 256, tokens)
     workgroups = pairs // groups
     assert pairs % groups == 0
     # at least one workgroup a compute unit when there are enough pairs; when a workgroup takes several pairs, no more
-    # workgroups than the picker aims at
+    # workgroups than the compute units hold at once
     assert workgroups >= min(pairs, 256)
-    assert groups == 1 or workgroups <= max(256, fused_blocks.ATTENTION_WORKGROUPS, pairs // 2)
+    assert groups == 1 or workgroups <= 256 * (8 // fused_blocks.attention_waves(positions, kv_heads, tokens, 64, 64)) * 2
 
 
 def test_attention_runs_at_the_timed_batches():
-    # batch 64: 256 workgroups of 2 pairs; batch 16: one pair a workgroup; batch 1024: 1,024 workgroups of 8
-    assert [groups_per_workgroup(b, 8, 256) for b in (16, 64, 1024)] == [1, 2, 8]
+    # batch 16: one pair a workgroup; batch 64: 256 workgroups of 2; batch 1024 (the split slab, two workgroups a compute
+    # unit): 512 workgroups of 16
+    assert [groups_per_workgroup(b, 8, 256) for b in (16, 64, 1024)] == [1, 2, 16]
+    assert [fused_blocks.attention_waves(b, 8, 70, 64, 64) for b in (64, 511, 512)] == [5, 5, 4]
+    # the split slab takes 65 to 80 tokens and widths up to 64
+    assert [fused_blocks.attention_waves(1024, 8, t, 64, dv) for t, dv in ((64, 64), (81, 64), (80, 128), (65, 16))] == [4, 6, 5, 4]
 
 
 def test_the_move_tables_are_the_gathers_of_the_heads():

@@ -459,6 +459,19 @@ def test_groups_a_workgroup_change_no_bit(device):
         launch_template_attention(*arguments, groups_per_block=5)   # not a divisor of the 36 pairs
 
 
+@pytest.mark.parametrize("heads, kv_heads, dq, dv, tokens", [(8, 8, 64, 64, 70), (8, 4, 32, 32, 80), (4, 4, 16, 64, 65)])
+def test_the_split_slab_launch_gives_the_small_launchs_bits(device, heads, kv_heads, dq, dv, tokens):
+    """65 to 80 tokens: from 4,096 (position, key/value group) pairs a launch splits the slab past the squares over three
+    wavefronts; a position's rows are the same bits as in a launch of three positions, and the answer is the fp32 formula's."""
+    positions = fused_blocks.ATTENTION_SPLIT_PAIRS // kv_heads
+    arguments = attention_operands(device, positions, heads, kv_heads, dq, dv, seed=tokens, tokens=tokens)
+    split = template_attention(*arguments)
+    assert torch.allclose(split.float(), reference_attention(arguments), atol=1e-2)
+    for rows in (slice(0, 3), slice(positions - 3, positions)):
+        few = template_attention(arguments[0][rows].contiguous(), *arguments[1:])
+        assert torch.equal(few, split[rows]), rows
+
+
 def test_template_attention_refuses_what_it_cannot_take(device):
     projected, templates, q_gain, k_gain, *rest = attention_operands(device, 2, 8, 8, 64, 64)
     with pytest.raises(ValueError):
