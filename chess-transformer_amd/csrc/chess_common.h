@@ -66,57 +66,34 @@ DEVICE float lane_mirror8(float v) { return __int_as_float(__builtin_amdgcn_mov_
 DEVICE float lane_mirror16(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); }
 DEVICE float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
 
-// The balanced tree of adjacent lane pairs over the 64 lanes of a wavefront, every lane ending with the same bits
-// (a + b == b + a bitwise): pairs of lanes, of 2, 4 and 8 lanes, then of 16-lane rows. Once a group's lanes all hold
-// its partial, pairing lane i with 7 - i or 15 - i (DPP mirrors) adds the same two partials as lane i ^ 4 or i ^ 8;
-// the four rows' sums are then added as (r0 + r1) + (r2 + r3). VALU only: no LDS permutes.
-DEVICE float wave_sum(float v) {
+// The balanced tree of adjacent lane pairs over each group of LANES lanes (16, 32 or the wavefront's 64), every lane
+// of a group ending with the same bits (a + b == b + a bitwise): pairs of lanes, of 2, 4 and 8 lanes, then of 16-lane
+// rows. Once a group's lanes all hold its partial, pairing lane i with 7 - i or 15 - i (DPP mirrors) adds the same two
+// partials as lane i ^ 4 or i ^ 8; two rows' sums are then added by a lane-16 exchange, four as (r0 + r1) + (r2 + r3).
+template <int LANES> DEVICE float group_sum(float v) {
+    static_assert(LANES == 16 || LANES == 32 || LANES == 64, "groups of 16, 32 or 64 lanes");
     v = v + lane_xor1(v);
     v = v + lane_xor2(v);
     v = v + lane_mirror8(v);
     v = v + lane_mirror16(v);
-    return (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    if constexpr (LANES == 32) v = v + __shfl_xor(v, 16, 64);
+    if constexpr (LANES == 64) v = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    return v;
 }
 
-DEVICE float wave_max(float v) {
+template <int LANES> DEVICE float group_max(float v) {
+    static_assert(LANES == 16 || LANES == 32 || LANES == 64, "groups of 16, 32 or 64 lanes");
     v = fmaxf(v, lane_xor1(v));
     v = fmaxf(v, lane_xor2(v));
     v = fmaxf(v, lane_mirror8(v));
     v = fmaxf(v, lane_mirror16(v));
-    return fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+    if constexpr (LANES == 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (LANES == 64) v = fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+    return v;
 }
 
-// The RMS norm's factor of one row on a wavefront, C contiguous elements a lane (zeros past the row's D): the lane's
-// squares as a pairwise tree, the wavefront's balanced tree (wave_sum), then 1 / sqrt(total / D + eps).
-template <int C> DEVICE float rms_inverse(const float (&v)[C], int D, float eps) {
-    float squares[C];
-#pragma unroll
-    for (int i = 0; i < C; i++) squares[i] = v[i] * v[i];
-#pragma unroll
-    for (int width = C; width > 1; width >>= 1)
-#pragma unroll
-        for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
-    const float total = wave_sum(squares[0]);
-    return 1.0f / __builtin_sqrtf(total / (float)D + eps);
-}
-
-// One row of norm_quant's declared order on a wavefront (C elements a lane, as rms_inverse): y = (v * inverse) * gain,
-// absmax = max(max |y|, 1e-20), q = rint(y * (127 / absmax)). Returns absmax (the row's scale is absmax / 127).
-template <int C> DEVICE float norm_quant_row(const float (&v)[C], const float (&gain)[C], int D, float eps, int8_t (&q)[C]) {
-    const float inverse = rms_inverse<C>(v, D, eps);
-    float y[C];
-    float largest = 0.0f;
-#pragma unroll
-    for (int i = 0; i < C; i++) {
-        y[i] = (v[i] * inverse) * gain[i];
-        largest = fmaxf(largest, fabsf(y[i]));
-    }
-    const float absmax = fmaxf(wave_max(largest), 1e-20f);
-    const float inverse_step = 127.0f / absmax;
-#pragma unroll
-    for (int i = 0; i < C; i++) q[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
-    return absmax;
-}
+DEVICE float wave_sum(float v) { return group_sum<64>(v); }
+DEVICE float wave_max(float v) { return group_max<64>(v); }
 
 // Maps a workgroup id so that consecutive tiles land on one XCD: the hardware deals
 // workgroups to the 8 XCDs round-robin, and each XCD has its own L2.

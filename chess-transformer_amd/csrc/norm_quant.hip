@@ -3,17 +3,24 @@
 //   [mixed = f16((x * rs) + (original * is))]
 //   y = (x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain
 //   absmax = max(max |y|, 1e-20);  q = rint(y * (127 / absmax));  scale = absmax / 127
+// tree_sum is the balanced binary tree of adjacent pairs over the row zero-padded to a power of two.
 // Without the quantisation (QUANT false) the same kernel is the fp16 blocks' RMSNorm: out = f16(y), after the same
 // optional mix (model/fused_blocks.py:346-348 and :351, and the final norm at :863).
-// A wavefront takes R rows, one at a time, after loading all of them; a lane holds C = next_pow2(D) / 64
-// contiguous elements of a row (at least 1), sums its squares as a pairwise tree and the wavefront adds
-// the lanes' sums as a balanced tree of adjacent lanes, which is the balanced tree over the zero-padded row.
-// Bandwidth-bound: 16-byte loads and stores, R rows of loads in flight a wavefront.
+//
+// A row is taken by a group of LANES lanes: the whole wavefront, or 16 lanes for rows up to 512 in large launches, so
+// that a wavefront's instructions serve four rows at once and a row's reductions and divisions are paid once for four. A lane holds J chunks of W contiguous elements
+// (W = 8: 16 bytes of fp16), chunk j at chunk place j LANES + (its lane in the group), so that each load and store
+// instruction moves a run of whole chunks across the group. The squares are added within a chunk as a pairwise tree,
+// the chunks of place j L .. j L + L - 1 across the group's lanes as a balanced tree of adjacent lanes (L = LANES), then
+// the J partials in the lane as a pairwise tree: the levels of the balanced tree over the padded row, in its order.
+// Bandwidth-bound: 16-byte loads and stores, R groups of rows of loads in flight a wavefront.
 #include "chess_common.h"
 
 namespace {
 
-constexpr int WAVES = 4;   // wavefronts a workgroup
+constexpr int WAVES = 4;             // wavefronts a workgroup
+constexpr int GROUPED_ROWS = 16384;  // from this many rows, rows up to 512 take groups of 16 lanes
+constexpr int WIDE_ROWS = 32768;     // from this many rows, rows taken by a whole wavefront go two a wavefront
 
 // naturally aligned vector types of 1 to 16 bytes: a copy of BYTES is one load or store of that width
 typedef unsigned v2u __attribute__((ext_vector_type(2)));
@@ -26,58 +33,106 @@ template <> struct Bytes<8> { typedef v2u type; };
 template <> struct Bytes<16> { typedef v4u type; };
 
 template <int BYTES> DEVICE void copy_bytes(void* to, const void* from) {
-    if constexpr (BYTES <= 16) {
-        *reinterpret_cast<typename Bytes<BYTES>::type*>(to) = *reinterpret_cast<const typename Bytes<BYTES>::type*>(from);
-    } else {
+    static_assert(BYTES <= 16, "one load or store");
+    *reinterpret_cast<typename Bytes<BYTES>::type*>(to) = *reinterpret_cast<const typename Bytes<BYTES>::type*>(from);
+}
+
+// A lane's share of a row: J chunks of W elements, chunk j's first column (j LANES + place) W, place = lane % LANES.
+template <int C, int LANES> struct Split {
+    static constexpr int W = C < 8 ? C : 8;
+    static constexpr int J = C / W;
+    static DEVICE int column(int j, int place) { return (j * LANES + place) * W; }
+};
+
+// The lane's C halves of a row (the caller zeroes those past D): a vector load a chunk when the row length is a
+// multiple of W, from a place clamped into the row, so that no branch holds the load back and the loads of several
+// rows stay in flight together; else element by element.
+template <int C, int LANES, bool VECTOR> DEVICE void load_raw(const half_t* row, int place, int D, half_t (&raw)[C]) {
+    typedef Split<C, LANES> S;
 #pragma unroll
-        for (int i = 0; i < BYTES / 16; i++) reinterpret_cast<v4u*>(to)[i] = reinterpret_cast<const v4u*>(from)[i];
+    for (int j = 0; j < S::J; j++) {
+        const int col = S::column(j, place);
+        if constexpr (VECTOR) {
+            copy_bytes<2 * S::W>(raw + j * S::W, row + min(col, D - S::W));
+        } else {
+#pragma unroll
+            for (int e = 0; e < S::W; e++) raw[j * S::W + e] = row[min(col + e, D - 1)];
+        }
     }
 }
 
-// C halves from row[col..col+C) (the caller zeroes those past D): one vector load when the row length is a multiple
-// of C, from a place clamped into the row, so that no branch holds the load back and the loads of several rows stay in
-// flight together; else element by element.
-template <int C, bool VECTOR> DEVICE void load_raw(const half_t* row, int col, int D, half_t (&raw)[C]) {
-    if constexpr (VECTOR) {
-        copy_bytes<2 * C>(raw, row + min(col, D - C));
-    } else {
+// FULL: the row is exactly the group's chunks (D == LANES C), so no element is past the row and nothing is masked
+template <int C, int LANES, bool FULL> DEVICE void widen(const half_t (&raw)[C], int place, int D, float (&out)[C]) {
+    typedef Split<C, LANES> S;
 #pragma unroll
-        for (int i = 0; i < C; i++) raw[i] = row[min(col + i, D - 1)];
+    for (int j = 0; j < S::J; j++)
+#pragma unroll
+        for (int e = 0; e < S::W; e++) out[j * S::W + e] = FULL || S::column(j, place) + e < D ? (float)raw[j * S::W + e] : 0.0f;
+}
+
+// the lane's C values of a row to it: a vector store a chunk when VECTOR, else element by element within the row
+template <int C, int LANES, bool VECTOR, bool FULL, typename T> DEVICE void store_row(T* row, int place, int D, const T (&values)[C]) {
+    typedef Split<C, LANES> S;
+#pragma unroll
+    for (int j = 0; j < S::J; j++) {
+        const int col = S::column(j, place);
+        if constexpr (VECTOR) {
+            if (FULL || col < D) copy_bytes<sizeof(T) * S::W>(row + col, values + j * S::W);
+        } else {
+#pragma unroll
+            for (int e = 0; e < S::W; e++)
+                if (col + e < D) row[col + e] = values[j * S::W + e];
+        }
     }
 }
 
-// FULL: the row is exactly 64 lanes of C (D == 64 C), so no element is past the row and nothing is masked
-template <int C, bool FULL> DEVICE void widen(const half_t (&raw)[C], int col, int D, float (&out)[C]) {
+// 1 / sqrt(tree_sum(v * v) / D + eps) of the group's row
+template <int C, int LANES> DEVICE float row_inverse(const float (&v)[C], int D, float eps) {
+    typedef Split<C, LANES> S;
+    float partial[S::J];
 #pragma unroll
-    for (int i = 0; i < C; i++) out[i] = FULL || col + i < D ? (float)raw[i] : 0.0f;
+    for (int j = 0; j < S::J; j++) {
+        float squares[S::W];
+#pragma unroll
+        for (int e = 0; e < S::W; e++) squares[e] = v[j * S::W + e] * v[j * S::W + e];
+#pragma unroll
+        for (int width = S::W; width > 1; width >>= 1)
+#pragma unroll
+            for (int i = 0; i < width / 2; i++) squares[i] = squares[2 * i] + squares[2 * i + 1];
+        partial[j] = group_sum<LANES>(squares[0]);
+    }
+#pragma unroll
+    for (int width = S::J; width > 1; width >>= 1)
+#pragma unroll
+        for (int i = 0; i < width / 2; i++) partial[i] = partial[2 * i] + partial[2 * i + 1];
+    return 1.0f / __builtin_sqrtf(partial[0] / (float)D + eps);
 }
 
-template <int C, int R, bool VECTOR, bool QUANT, bool FULL = false>
+template <int C, int LANES, int R, bool VECTOR, bool QUANT, bool FULL = false>
 __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
     const half_t* __restrict__ x, const half_t* __restrict__ original, const half_t* __restrict__ residual_scale,
     const half_t* __restrict__ input_scale, const half_t* __restrict__ gain, half_t* __restrict__ mixed,
     int8_t* __restrict__ q, float* __restrict__ scale, half_t* __restrict__ normed, int M, int D, float eps, int mix)
 {
+    constexpr int GROUPS = 64 / LANES;   // rows a wavefront takes at once
     const int lane = threadIdx.x & 63;
-    const int first = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R;
+    const int first = (blockIdx.x * WAVES + (threadIdx.x >> 6)) * R * GROUPS;
     if (first >= M) return;  // the whole wavefront leaves together
-    constexpr bool vector = VECTOR;
-    const int col = lane * C;
+    const int group = lane / LANES, place = lane % LANES;
 
-    // the wavefront's R rows (and inputs) are loaded before any is used, so that R rows of loads are in flight
+    // the wavefront's R x GROUPS rows (and inputs) are loaded before any is used, so that all their loads are in flight
     half_t raw_x[R][C], raw_o[R][C];
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int row = min(first + r, M - 1);
-        load_raw<C, VECTOR>(x + (size_t)row * D, col, D, raw_x[r]);
-        if (mix) load_raw<C, VECTOR>(original + (size_t)row * D, col, D, raw_o[r]);
+        const int row = min(first + r * GROUPS + group, M - 1);
+        load_raw<C, LANES, VECTOR>(x + (size_t)row * D, place, D, raw_x[r]);
+        if (mix) load_raw<C, LANES, VECTOR>(original + (size_t)row * D, place, D, raw_o[r]);
     }
-    // the gain: one vector load when the row is full (the launch checks its alignment), else element by element
+    // the gain: vector loads when the row is full (the launch checks its alignment), else element by element
     half_t raw_g[C];
-    if constexpr (FULL) copy_bytes<2 * C>(raw_g, gain + col);
-    else load_raw<C, false>(gain, col, D, raw_g);
+    load_raw<C, LANES, FULL>(gain, place, D, raw_g);
     float g[C];
-    widen<C, FULL>(raw_g, col, D, g);
+    widen<C, LANES, FULL>(raw_g, place, D, g);
     float rs = 0.0f, is = 0.0f;
     if (mix) {
         rs = (float)residual_scale[0];
@@ -86,42 +141,44 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
 
 #pragma unroll
     for (int r = 0; r < R; r++) {
-        const int row = first + r;
-        if (row >= M) break;
-        const size_t base = (size_t)row * D;
+        // every lane takes part in its group's reductions; the lanes of rows past M (which read row M - 1) store nothing
+        if (first + r * GROUPS >= M) break;
+        const int row = first + r * GROUPS + group;
+        const bool live = row < M;
+        const size_t base = (size_t)min(row, M - 1) * D;
         float v[C];
-        widen<C, FULL>(raw_x[r], col, D, v);
+        widen<C, LANES, FULL>(raw_x[r], place, D, v);
         if (mix) {
             float o[C];
-            widen<C, FULL>(raw_o[r], col, D, o);
+            widen<C, LANES, FULL>(raw_o[r], place, D, o);
             half_t m[C];
 #pragma unroll
             for (int i = 0; i < C; i++) {
                 m[i] = (half_t)((v[i] * rs) + (o[i] * is));
                 v[i] = (float)m[i];
             }
-            if (vector) {
-                if (FULL || col < D) copy_bytes<2 * C>(mixed + base + col, m);
-            } else {
-#pragma unroll
-                for (int i = 0; i < C; i++)
-                    if (col + i < D) mixed[base + col + i] = m[i];
-            }
+            if (live) store_row<C, LANES, VECTOR, FULL>(mixed + base, place, D, m);
         }
 
+        const float inverse = row_inverse<C, LANES>(v, D, eps);
         if constexpr (QUANT) {
-            int8_t out[C];
-            const float absmax = norm_quant_row<C>(v, g, D, eps, out);
-            if (vector) {
-                if (FULL || col < D) copy_bytes<C>(q + base + col, out);
-            } else {
+            float y[C];
+            float largest = 0.0f;
 #pragma unroll
-                for (int i = 0; i < C; i++)
-                    if (col + i < D) q[base + col + i] = out[i];
+            for (int i = 0; i < C; i++) {
+                y[i] = (v[i] * inverse) * g[i];
+                largest = fmaxf(largest, fabsf(y[i]));
             }
-            if (lane == 0) scale[row] = absmax / 127.0f;
+            const float absmax = fmaxf(group_max<LANES>(largest), 1e-20f);
+            const float inverse_step = 127.0f / absmax;
+            int8_t out[C];
+#pragma unroll
+            for (int i = 0; i < C; i++) out[i] = (int8_t)(int)__builtin_rintf(y[i] * inverse_step);
+            if (live) {
+                store_row<C, LANES, VECTOR, FULL>(q + base, place, D, out);
+                if (place == 0) scale[row] = absmax / 127.0f;
+            }
         } else {
-            const float inverse = rms_inverse<C>(v, D, eps);
             half_t out[C];
 #pragma unroll
             for (int i = 0; i < C; i++) {
@@ -129,53 +186,56 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
                 asm volatile("" : "+v"(y));   // the f32 product rounds to fp16 (one rounding of y, not a mixed multiply)
                 out[i] = (half_t)y;
             }
-            if (vector) {
-                if (FULL || col < D) copy_bytes<2 * C>(normed + base + col, out);
-            } else {
-#pragma unroll
-                for (int i = 0; i < C; i++)
-                    if (col + i < D) normed[base + col + i] = out[i];
-            }
+            if (live) store_row<C, LANES, VECTOR, FULL>(normed + base, place, D, out);
         }
     }
 }
 
-template <int C, bool QUANT>
+// Timed on an MI355X, norm_quant of rows of 512 (us, 16 lanes a row against the whole wavefront): 71,680 rows 20.9 against
+// 27.5, 17,920 rows 7.3 against 8.8, 4,480 rows 3.79 against 3.84, 70 rows 2.74 against 2.25; the fp16 blocks' RMSNorm
+// 3.51 against 3.21 at 4,480 rows. A whole wavefront a row at 32,768 rows and more: two rows a wavefront (at 71,680 rows
+// of 512, 29.1 us against 41.5 for one).
+template <int C, int LANES, bool QUANT>
 int launch(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
            void* q, void* scale, void* normed, int M, int D, float eps, hipStream_t stream)
 {
-    // rows a wavefront: two once the launch fills the chip (at 71,680 rows of 512 one row takes 41.5 us, two 29.1, four
-    // 30.0, eight 31.2 on an MI355X), one row a wavefront while it does not
-    constexpr int WIDE = 2;
-    const bool wide = M >= 32768;
-    const int rows_per_block = WAVES * (wide ? WIDE : 1);
+    constexpr int GROUPS = 64 / LANES;
+    const bool wide = LANES == 64 && M >= WIDE_ROWS;
+    const int rows_per_block = WAVES * GROUPS * (wide ? 2 : 1);
     const dim3 grid((M + rows_per_block - 1) / rows_per_block), block(64 * WAVES);
-    // a full row (D == 64 C) with a 16-byte aligned gain takes no masks and loads the gain as vectors (at 71,680 rows
-    // of 512 on an MI355X: 28.8 us, from 32.5 us with the masks and the gain's element loads)
-    const bool full = D == 64 * C && aligned16(gain);
-    auto kernel = wide ? (full ? norm_quant_kernel<C, WIDE, true, QUANT, true>
-                               : D % C == 0 ? norm_quant_kernel<C, WIDE, true, QUANT> : norm_quant_kernel<C, WIDE, false, QUANT>)
-                       : (full ? norm_quant_kernel<C, 1, true, QUANT, true>
-                               : D % C == 0 ? norm_quant_kernel<C, 1, true, QUANT> : norm_quant_kernel<C, 1, false, QUANT>);
+    // a full row (D == LANES C) with a 16-byte aligned gain takes no masks and loads the gain as vectors
+    const bool full = D == LANES * C && aligned16(gain);
+    const bool vector = D % Split<C, LANES>::W == 0;
+    auto kernel = wide ? (full ? norm_quant_kernel<C, LANES, 2, true, QUANT, true>
+                               : vector ? norm_quant_kernel<C, LANES, 2, true, QUANT> : norm_quant_kernel<C, LANES, 2, false, QUANT>)
+                       : (full ? norm_quant_kernel<C, LANES, 1, true, QUANT, true>
+                               : vector ? norm_quant_kernel<C, LANES, 1, true, QUANT> : norm_quant_kernel<C, LANES, 1, false, QUANT>);
     hipLaunchKernelGGL(kernel, grid, block, 0, stream, (const half_t*)x, (const half_t*)original, (const half_t*)residual_scale,
                        (const half_t*)input_scale, (const half_t*)gain, (half_t*)mixed, (int8_t*)q, (float*)scale, (half_t*)normed, M, D,
                        eps, original != nullptr ? 1 : 0);
     return launch_status();
 }
 
+// rows up to 512 (zero-padded to a power of two) in launches of GROUPED_ROWS or more take groups of 16 lanes, 4 to 32
+// elements a lane; else a whole wavefront a row, 1 to 32 elements a lane. Any split gives the same bits.
 template <bool QUANT>
 int by_width(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed, void* q,
              void* scale, void* normed, int M, int D, float eps, hipStream_t s)
 {
     int padded = 64;
     while (padded < D) padded <<= 1;
-    switch (padded / 64) {
-        case 1: return launch<1, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
-        case 2: return launch<2, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
-        case 4: return launch<4, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
-        case 8: return launch<8, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
-        case 16: return launch<16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
-        default: return launch<32, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+    const bool grouped = M >= GROUPED_ROWS;
+    switch (padded) {
+        case 64: return grouped ? launch<4, 16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s)
+                                : launch<1, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 128: return grouped ? launch<8, 16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s)
+                                 : launch<2, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 256: return grouped ? launch<16, 16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s)
+                                 : launch<4, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 512: return grouped ? launch<32, 16, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s)
+                                 : launch<8, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        case 1024: return launch<16, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
+        default: return launch<32, 64, QUANT>(x, original, residual_scale, input_scale, gain, mixed, q, scale, normed, M, D, eps, s);
     }
 }
 

@@ -48,7 +48,7 @@ def test_norm_quant_matches_the_oracle_to_the_bit(device, D, mix):
     assert bits_equal(q, expected_q) and bits_equal(scale, expected_scale)
 
 
-@pytest.mark.parametrize("rows, D", [(210, 128), (210, 192), (210, 512), (210, 768), (40000, 512)])
+@pytest.mark.parametrize("rows, D", [(210, 128), (210, 192), (210, 512), (210, 768), (40000, 512), (16384, 192), (20000, 96), (33000, 768)])
 @pytest.mark.parametrize("mix", [False, True])
 def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
     """The fp16 blocks' norm (and their own input mix): the oracle's bits, one row a wavefront and (40,000 rows) two;
@@ -70,6 +70,27 @@ def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
     assert normed.dtype == torch.float16 and bits_equal(normed, expected)
     torchs = F.rms_norm(rows_in.float(), (D,), gain.float(), 1e-5)
     assert ((normed.float() - torchs).abs() <= torchs.half().abs().float() * 2 ** -10 + 2 ** -24).all()
+
+
+@pytest.mark.parametrize("rows, D", [(16384, 192), (20000, 96), (16400, 64), (33000, 768), (32768, 2048)])
+@pytest.mark.parametrize("mix", [False, True])
+def test_norm_quant_of_large_launches_matches_the_oracle_to_the_bit(device, rows, D, mix):
+    """From 16,384 rows, rows up to 512 take groups of 16 lanes (four rows a wavefront, chunks strided across the group,
+    masked past rows that are no power of two); longer rows a wavefront each, two a wavefront from 32,768 rows. Every
+    split adds the same balanced tree, so the bits are the oracle's."""
+    generator = torch.Generator(device="cpu").manual_seed(rows + D)
+    x = (torch.randn(rows, D, generator=generator) * 4).half()
+    original = torch.randn(rows, D, generator=generator).half()
+    gain = (torch.rand(D, generator=generator) + 0.5).half()
+    rs, is_ = torch.tensor([0.8]).half(), torch.tensor([0.5]).half()
+    if mix:
+        mixed, q, scale = mix_norm_quant(x.to(device), original.to(device), rs.to(device), is_.to(device), gain.to(device), 1e-5)
+        expected_mixed, expected_q, expected_scale = oracle.mix_norm_quant(x.numpy(), original.numpy(), rs.numpy(), is_.numpy(), gain.numpy(), 1e-5)
+        assert bits_equal(mixed, expected_mixed)
+    else:
+        q, scale = norm_quant(x.to(device), gain.to(device), 1e-5)
+        expected_q, expected_scale = oracle.norm_quant(x.numpy(), gain.numpy(), 1e-5)
+    assert bits_equal(q, expected_q) and bits_equal(scale, expected_scale)
 
 
 def test_norm_quant_rounds_the_rmsnorm(device):
