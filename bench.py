@@ -337,8 +337,10 @@ def kernel_role(name: str) -> str:
             return "fp16 block gate_up"
         return {"3": "combine (fp16, bias + residual)", "1": "fp16 block projection", "2": "fp16 block down",
                 "6": "fp16 block down (mix)"}.get(epilogue, "fp16 gemm")
-    for key, role in (("norm_quant_kernelILi8ELi1ELb1ELb0", "rms_norm (fp16 block, final norm)"), ("norm_quant_kernelILi8ELi2ELb1ELb0", "rms_norm (fp16 block, final norm)"),
-                      ("norm_quant_kernel", "norm_quant"), ("rotate_quant", "rotate_quant"), ("template_attention", "template_attention"),
+    found = re.search(r"norm_quant_kernelILi\d+ELi\d+ELi\d+ELb\dELb(\d)", name)
+    if found:   # template arguments C, LANES, R, VECTOR, QUANT, FULL: without QUANT it is the fp16 blocks' RMSNorm
+        return "norm_quant" if found.group(1) == "1" else "rms_norm (fp16 block, final norm)"
+    for key, role in (("norm_quant_kernel", "norm_quant"), ("rotate_quant", "rotate_quant"), ("template_attention", "template_attention"),
                       ("board_embedding", "board_embedding"), ("head_blocks", "move logits: product blocks"), ("head_gather", "move logits: gather"),
                       ("move_logits", "move_logits"), ("value_hidden", "value_hidden"),
                       ("value_score", "value_score"), ("copy", "copy")):
@@ -358,8 +360,14 @@ def counter_summary(folder: Path) -> int:
     import csv
     values: dict[str, dict[str, list[float]]] = {}
     for path in sorted(folder.rglob("*counter_collection.csv")):
-        for row in csv.DictReader(path.open()):
-            values.setdefault(kernel_role(row["Kernel_Name"]), {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
+        rows = list(csv.DictReader(path.open()))
+        number = "Dispatch_Id" if rows and "Dispatch_Id" in rows[0] else "Correlation_Id"
+        # the forwards' dispatches only (from the first input embedding on), not the network's set-up on the GPU
+        embeddings = [int(row[number]) for row in rows if kernel_role(row["Kernel_Name"]) == "board_embedding"]
+        first = min(embeddings) if embeddings else 0
+        for row in rows:
+            if int(row[number]) >= first:
+                values.setdefault(kernel_role(row["Kernel_Name"]), {}).setdefault(row["Counter_Name"], []).append(float(row["Counter_Value"]))
     columns = ["dispatch cycles", "int8 MFMA % of peak", "MFMA busy %", "VALU busy %", "MFMA co-exec with VALU %",
                "L2 requests /cycle/channel", "L2 hit %", "TA busy %", "VALU instr /wave", "MFMA instr /wave", "transcendental /wave",
                "waiting cycles /wave", "wave cycles /wave", "FETCH_SIZE KiB", "WRITE_SIZE KiB"]
