@@ -11,7 +11,8 @@
 // model/attention_cuda.py:410-440).
 //
 // A workgroup takes a run of groups_per_block (position, key/value group) pairs, in order, which may run on
-// from one position into the next; it has one wavefront per slab of 16 queries. A group's raw key, value and
+// from one position into the next; it has one wavefront per slab of 16 queries, or (SPLIT, five slabs in large
+// launches) four wavefronts, three of which share the fifth slab by 32-key step. A group's raw key, value and
 // query rows arrive by DMA into LDS, double-buffered: the next group's rows load while this group's heads run.
 // A wavefront then runs each head of the group on v_mfma_f32_16x16x32_f16: the scores come out transposed,
 // S^T = K Q^T, from the raw keys and a per-key scale, so a lane holds one query's scores for 4 keys of each
@@ -130,7 +131,9 @@ template <int CH> DEVICE int raw_slot(int row, int chunk) { return row * CH + (c
 // A wavefront's share of the DMA of a raw block of ROWS rows x CH 16-byte chunks, 64 chunks an instruction:
 // instruction i = wave + j WAVES writes slots i * 64 + lane, slot s holding chunk (s % CH) ^ swizzle(row) of row
 // s / CH. The lane's source offsets (halves from the block's first column) are planned once: rows past last read
-// row last again (their values are masked or multiplied by zero later), so every address is inside the rows.
+// row last again (their values are masked or multiplied by zero later), so every address is inside the rows. The
+// offsets are in bytes, so that a load's address is the block's (uniform) start plus the lane's 32-bit offset: the
+// scalar-base form of the DMA, with no 64-bit address arithmetic in the lanes.
 template <int ROWS, int CH, int WAVES>
 struct DmaPlan {
     static constexpr int INSTRUCTIONS = ROWS * CH / 64;
@@ -141,15 +144,16 @@ struct DmaPlan {
 #pragma unroll
         for (int j = 0; j < PER_WAVE; j++) {
             const int slot = (wave + j * WAVES) * 64 + lane, row = min(slot / CH, ROWS - 1), chunk = (slot % CH) ^ swizzle<CH>(row);
-            offset[j] = (uint32_t)(min(row, last) * stride + chunk * 8);
+            offset[j] = (uint32_t)(min(row, last) * stride + chunk * 8) * 2u;
         }
     }
     DEVICE void issue(LDS_SPACE int8_t* raw, const half_t* source, int wave) const {
+        const int8_t* bytes = reinterpret_cast<const int8_t*>(source);
 #pragma unroll
         for (int j = 0; j < PER_WAVE; j++) {
             const int i = wave + j * WAVES;
             if (INSTRUCTIONS % WAVES == 0 || i < INSTRUCTIONS)
-                __builtin_amdgcn_global_load_lds((const void*)(source + offset[j]), (LDS_SPACE void*)(raw + i * 1024), 16, 0, 0);
+                __builtin_amdgcn_global_load_lds((const void*)(bytes + offset[j]), (LDS_SPACE void*)(raw + i * 1024), 16, 0, 0);
         }
     }
 };
@@ -196,7 +200,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
     DmaPlan<L::VKEYS, VC, WAVES> value_plan;
     key_plan.plan(T - 1, width, slab, lane);
     value_plan.plan(T - 1, width, slab, lane);
-    const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset);   // a square query's row, for the coefficients' DMA
+    const uint32_t coefficient_row = (uint32_t)(lane * width + c_offset) * 2u;   // a square query's row (bytes), for the coefficients' DMA
 
     // a pair's keys and values (kv), its queries and coefficients (q), into a buffer
     auto dma_group = [&](int pair, int buffer, bool kv, bool q) {
@@ -211,7 +215,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                 key_plan.issue(raw_q + (buffer * per_kv + hi) * head_bytes, board + (group * per_kv + hi) * dq, slab);
             if (templates_count == MAX_TEMPLATES) {
                 for (int hi = slab; hi < per_kv; hi += WAVES)
-                    __builtin_amdgcn_global_load_lds((const void*)(board + coefficient_row + (group * per_kv + hi) * MAX_TEMPLATES),
+                    __builtin_amdgcn_global_load_lds((const void*)(reinterpret_cast<const int8_t*>(board + (group * per_kv + hi) * MAX_TEMPLATES) + coefficient_row),
                                                      (LDS_SPACE void*)(raw_c + (buffer * per_kv + hi) * L::COEF_BYTES), 16, 0, 0);
             }
         }

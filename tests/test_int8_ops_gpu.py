@@ -51,7 +51,8 @@ def test_norm_quant_matches_the_oracle_to_the_bit(device, D, mix):
 @pytest.mark.parametrize("rows, D", [(210, 128), (210, 192), (210, 512), (210, 768), (40000, 512), (16384, 192), (20000, 96), (33000, 768)])
 @pytest.mark.parametrize("mix", [False, True])
 def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
-    """The fp16 blocks' norm (and their own input mix): the oracle's bits, one row a wavefront and (40,000 rows) two;
+    """The fp16 blocks' norm (and their own input mix): the oracle's bits, a wavefront a row (210 rows), 16-lane groups of
+    four rows a wavefront (from 16,384 rows, rows up to 512) and two whole-wavefront rows a wavefront (33,000 rows of 768);
     within one fp16 rounding of torch's rms_norm in f32 (the reference's nn.RMSNorm)."""
     torch.manual_seed(rows + D)
     x = (torch.randn(rows, D, device=device) * 4).half()
