@@ -366,8 +366,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                 if (c * 8 >= dq) qv[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
                 squares = squares8(qv[ks], squares);
             }
-            squares += __shfl_xor(squares, 16, 64);
-            squares += __shfl_xor(squares, 32, 64);
+            squares = sum_across_rows(squares);
             const float q_inverse = 1.0f / __builtin_sqrtf(squares / columns + eps);
             v8h qf[DQP / 32];
 #pragma unroll
@@ -418,8 +417,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                     top = fmaxf(top, value);
                 }
             }
-            top = fmaxf(top, __shfl_xor(top, 16, 64));
-            top = fmaxf(top, __shfl_xor(top, 32, 64));
+            top = max_across_rows(top);
             float total = 0.0f;
             const float offset = -top * LOG2E;
             if constexpr (L::BY_STEP) {
@@ -435,8 +433,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                             s[kt][r] = p;
                             step_total += p;
                         }
-                    step_total += __shfl_xor(step_total, 16, 64);
-                    step_total += __shfl_xor(step_total, 32, 64);
+                    step_total = sum_across_rows(step_total);
                     total = st == 0 ? step_total : total + step_total;
                 }
             } else {
@@ -448,8 +445,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                         s[kt][r] = p;
                         total += p;
                     }
-                total += __shfl_xor(total, 16, 64);
-                total += __shfl_xor(total, 32, 64);
+                total = sum_across_rows(total);
             }
             const float inverse_total = __builtin_amdgcn_rcpf(total);
 
@@ -534,8 +530,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                         if (c * 8 >= dq) mq[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
                         msquares = squares8(mq[ks], msquares);
                     }
-                    msquares += __shfl_xor(msquares, 16, 64);
-                    msquares += __shfl_xor(msquares, 32, 64);
+                    msquares = sum_across_rows(msquares);
                     const float mq_inverse = 1.0f / __builtin_sqrtf(msquares / columns + eps);
 #pragma unroll
                     for (int ks = 0; ks < DQP / 32; ks++)
@@ -563,8 +558,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                             mtop = fmaxf(mtop, value);
                         }
                     }
-                    mtop = fmaxf(mtop, __shfl_xor(mtop, 16, 64));
-                    mtop = fmaxf(mtop, __shfl_xor(mtop, 32, 64));
+                    mtop = max_across_rows(mtop);
                     if (quad == 0) meta_max[part * 16 + col] = mtop;
                 }
                 lds_barrier();   // the parts' maxima are in place
@@ -580,8 +574,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                             ms[h2][r] = p;
                             mtotal += p;
                         }
-                    mtotal += __shfl_xor(mtotal, 16, 64);
-                    mtotal += __shfl_xor(mtotal, 32, 64);
+                    mtotal = sum_across_rows(mtotal);
                     if (quad == 0) meta_sum[part * 16 + col] = mtotal;
                     v8h pf;
 #pragma unroll

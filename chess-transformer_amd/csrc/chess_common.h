@@ -64,20 +64,44 @@ DEVICE float lane_xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp
 // lane 7 - i and lane 15 - i of each 8 and 16 lanes by DPP mirrors (row_half_mirror, row_mirror)
 DEVICE float lane_mirror8(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)); }
 DEVICE float lane_mirror16(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); }
-DEVICE float lane_value(float v, int lane) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane)); }
+
+// Lanes l and l ^ 16 (rows of 16 lanes paired 0-1, 2-3), and l and l ^ 32, exchanged by VALU lane swaps
+// (v_permlane16_swap, v_permlane32_swap) instead of an LDS permute: with the value as both operands, the swap leaves
+// the pair's first value in one result and its second in the other, in every lane of the pair, so that
+// first + second (or their max) is the same bits in both lanes, and the same bits as v + v[l ^ 16] (a + b == b + a).
+DEVICE float sum_rows16(float v) {
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
+DEVICE float sum_halves32(float v) {
+    const auto pair = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(pair[0]) + __uint_as_float(pair[1]);
+}
+DEVICE float max_rows16(float v) {
+    const auto pair = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(pair[0]), __uint_as_float(pair[1]));
+}
+DEVICE float max_halves32(float v) {
+    const auto pair = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(pair[0]), __uint_as_float(pair[1]));
+}
+// over the four lanes l, l ^ 16, l ^ 32, l ^ 48: the pairs of 16 first, then of 32
+DEVICE float sum_across_rows(float v) { return sum_halves32(sum_rows16(v)); }
+DEVICE float max_across_rows(float v) { return max_halves32(max_rows16(v)); }
 
 // The balanced tree of adjacent lane pairs over each group of LANES lanes (16, 32 or the wavefront's 64), every lane
 // of a group ending with the same bits (a + b == b + a bitwise): pairs of lanes, of 2, 4 and 8 lanes, then of 16-lane
 // rows. Once a group's lanes all hold its partial, pairing lane i with 7 - i or 15 - i (DPP mirrors) adds the same two
-// partials as lane i ^ 4 or i ^ 8; two rows' sums are then added by a lane-16 exchange, four as (r0 + r1) + (r2 + r3).
+// partials as lane i ^ 4 or i ^ 8; two rows' sums are then added by a lane-16 swap, four as (r0 + r1) + (r2 + r3) by
+// the 16- and 32-lane swaps. VALU only: no LDS permutes.
 template <int LANES> DEVICE float group_sum(float v) {
     static_assert(LANES == 16 || LANES == 32 || LANES == 64, "groups of 16, 32 or 64 lanes");
     v = v + lane_xor1(v);
     v = v + lane_xor2(v);
     v = v + lane_mirror8(v);
     v = v + lane_mirror16(v);
-    if constexpr (LANES == 32) v = v + __shfl_xor(v, 16, 64);
-    if constexpr (LANES == 64) v = (lane_value(v, 0) + lane_value(v, 16)) + (lane_value(v, 32) + lane_value(v, 48));
+    if constexpr (LANES == 32) v = sum_rows16(v);
+    if constexpr (LANES == 64) v = sum_across_rows(v);   // (r0 + r1) + (r2 + r3)
     return v;
 }
 
@@ -87,8 +111,8 @@ template <int LANES> DEVICE float group_max(float v) {
     v = fmaxf(v, lane_xor2(v));
     v = fmaxf(v, lane_mirror8(v));
     v = fmaxf(v, lane_mirror16(v));
-    if constexpr (LANES == 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-    if constexpr (LANES == 64) v = fmaxf(fmaxf(lane_value(v, 0), lane_value(v, 16)), fmaxf(lane_value(v, 32), lane_value(v, 48)));
+    if constexpr (LANES == 32) v = max_rows16(v);
+    if constexpr (LANES == 64) v = max_across_rows(v);
     return v;
 }
 
