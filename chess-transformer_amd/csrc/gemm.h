@@ -7,7 +7,7 @@
 namespace gemm {
 
 constexpr int STAGE_K_BYTES = 64;
-constexpr int TILES = 14;       // tiles 1 to 14 (12 is not one; 14 splits K, int8 only); 0 picks by size
+constexpr int TILES = 14;       // tiles 1 to 14 (14 splits K, int8 only); 0 picks by size
 constexpr int FIRST_SPLIT = 14;
 
 enum { EPI_BIAS = 1, EPI_RESIDUAL = 2, EPI_MIX = 4 };

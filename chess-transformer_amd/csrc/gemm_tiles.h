@@ -464,8 +464,8 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (2 x 2, 3)  5: 128 x 256 (2 x 2, 3)   6: 256 x 64 (4 x 1, 4)
 // 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
-// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2)  13: 128 x 128 (2 x 2, 2) with stages of 128 bytes of K (rows of a
-// multiple of 128 bytes). 0 picks by the launch's size; 12 is not a tile.
+// 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2)  12: 128 x 64 (2 x 2, 2) and 13: 128 x 128 (2 x 2, 2) with stages
+// of 128 bytes of K (rows of a multiple of 128 bytes). 0 picks by the launch's size.
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
 int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     switch (tile) {
@@ -479,6 +479,7 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
         case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 9: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 10: return launch<In, 256, 64, 4, 1, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 12: return launch<In, 128, 64, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);
         case 13: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);
         default: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
     }
@@ -500,7 +501,6 @@ template <typename In> int tile_by_size(int M, int N, int K) {
 template <typename In, int NB, typename OutT>
 int dispatch(const void* x, const void* w, void* out, const Epilogue& e, int M, int N, int K, int tile, hipStream_t stream) {
     if (tile == 0) tile = tile_by_size<In>(M, N, K);
-    if (tile == 12) return chess_fail(CHESS_UNSUPPORTED, "tile 12 is not a tile of this GEMM");
     if (tile >= FIRST_SPLIT) {
         if constexpr (std::is_same<In, int8_t>::value) return split::dispatch<NB, OutT>(x, w, out, e, M, N, K, tile, stream);
         return chess_fail(CHESS_UNSUPPORTED, "the split-K tile %d is int8 only", FIRST_SPLIT);

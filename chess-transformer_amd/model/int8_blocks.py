@@ -31,12 +31,13 @@ INT8_DEPTH = 64
 # for one or two positions, int8_cuda.py:34-183: in a kernel trace 3.6, 4.3 and 6.2 us where tile 1 takes 4.4, 5.2 and 7.6
 # for projection, gate_up and down at 70 rows; gate_up's tile 1 is faster again at 140 rows, the others from about 200).
 # down takes tile 11 up to 160 rows a compute unit and 13 past it (the network at batch 256 / 512 / 1024: 6.63 / 12.11 /
-# 22.18 ms a forward with tile 11, 6.80 / 12.24 / 21.99 with 13). Between 4 and 9 rows a compute unit (batches 15 to 32)
+# 22.18 ms a forward with tile 11, 6.80 / 12.24 / 21.99 with 13), and 12 (128 x 64 with 128-byte stages) from 8 to 32
+# rows (batch 64: 2.478 against 2.500 ms a forward with tile 1; at batch 256 tile 11 stays ahead in the network). Between 4 and 9 rows a compute unit (batches 15 to 32)
 # projection takes tile 1 and then 8 (batch 16: 0.06 ms a forward faster than tile 11, batch 32: 0.035), and gate_up takes
 # tile 8 up to 18 rows (batch 16 / 32 / 64: 0.05 / 0.03 / 0.045 ms faster than tile 10). Every tile gives the same bits.
 INT8_TILES = {"gfx950": {"projection": [(0.55, 14), (5, 1), (9, 8), (math.inf, 11)],
                          "gate_up": [(0.3, 14), (4, 1), (18, 8), (math.inf, 10)],
-                         "down": [(0.55, 14), (32, 1), (160, 11), (math.inf, 13)]}}
+                         "down": [(0.55, 14), (8, 1), (32, 12), (160, 11), (math.inf, 13)]}}
 # the split-K tile's wavefronts: each reads 1, 2 or 4 steps of 128 bytes of K, and the outputs go 8 columns a lane
 SPLIT_WAVES = {14: 4}
 # rows a workgroup of the norm and rotation kernels (one wavefront a row); no count changes a bit

@@ -357,7 +357,7 @@ def test_the_config1_gemms_are_the_oracles_in_bf16(device, M, K, N):
     assert np.array_equal(cpu(out.float())[rows], expected)
 
 
-ALL_TILES = (*range(1, 12), 13)   # 12 is not a tile; 13 takes 128-byte stages
+ALL_TILES = tuple(range(1, 14))   # 12 and 13 take 128-byte stages
 SPLIT_TILES = (14,)              # int8 only
 
 
@@ -378,7 +378,7 @@ def test_every_tile_gives_the_same_bits(device, matmul):
 def test_128_byte_stages_refuse_rows_of_64(device):
     x, x_scale, weight, weight_scale, bias, residual, gated, mix = int8_operands("projection", 70, device, width=128, depth=192)
     launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, 1)   # 64-byte stages take it
-    for tile in (13,):
+    for tile in (12, 13):
         with pytest.raises(ValueError):
             launch_int8_linear(x, x_scale, weight, weight_scale, bias, residual, gated, *mix, tile)
 
