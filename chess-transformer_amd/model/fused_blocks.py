@@ -30,8 +30,9 @@ LINEAR_TILES = {"gfx950": [(5, 1), (9, 3), (18, 8), (math.inf, 11)]}
 # 97 us at 71,680 rows on an MI355X)
 LINEAR_F32_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
 # rows of 2 KB or more (the fp16 block's down, 2,048 inputs), not gated: 128 x 128 with 128-byte stages, whole L2 lines a
-# step (190 against 226 us at 71,680 rows)
-LINEAR_LONG_ROW_TILES = {"gfx950": [(4, 1), (math.inf, 13)]}
+# step (190 against 226 us at 71,680 rows); 128 x 64 with 128-byte stages up to 160 rows a compute unit (batch 64 / 256:
+# 22.0 / 57.6 against 23.8 / 58.0 us) and 64 x 64 up to 9 (batch 16: 11.8 against 20.7 us)
+LINEAR_LONG_ROW_TILES = {"gfx950": [(9, 1), (160, 12), (math.inf, 13)]}
 LONG_ROW_BYTES = 2048
 # from this many (position, key/value group) pairs a template_attention launch of 65 to 80 tokens, query and value widths
 # up to 64, splits the slab of the tokens past the squares over three wavefronts: workgroups of four wavefronts instead
