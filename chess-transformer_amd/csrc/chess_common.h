@@ -57,13 +57,15 @@ DEVICE float silu_fast(float g) {
     return g * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(g * -1.44269504f));
 }
 
-// lane ^ 1 and lane ^ 2 by DPP quad permutes (no LDS round trip): quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]
-DEVICE float lane_xor1(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false)); }
-DEVICE float lane_xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false)); }
+// lane ^ 1 and lane ^ 2 by DPP quad permutes (no LDS round trip): quad_perm [1, 0, 3, 2] and [2, 3, 0, 1]. These and
+// the mirrors below read a lane of the same row that always exists, so bound_ctrl (zero for a lane that does not) never
+// applies; set, it lets the compiler fold the move into the add or max that uses it (v_add_f32_dpp).
+DEVICE float lane_xor1(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true)); }
+DEVICE float lane_xor2(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true)); }
 
 // lane 7 - i and lane 15 - i of each 8 and 16 lanes by DPP mirrors (row_half_mirror, row_mirror)
-DEVICE float lane_mirror8(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false)); }
-DEVICE float lane_mirror16(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); }
+DEVICE float lane_mirror8(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, true)); }
+DEVICE float lane_mirror16(float v) { return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, true)); }
 
 // Lanes l and l ^ 16 (rows of 16 lanes paired 0-1, 2-3), and l and l ^ 32, exchanged by VALU lane swaps
 // (v_permlane16_swap, v_permlane32_swap) instead of an LDS permute: with the value as both operands, the swap leaves
