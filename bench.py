@@ -144,6 +144,32 @@ def time_kernel(launch, repeats: int = 30) -> float:
     return begin.elapsed_time(end) / repeats
 
 
+def time_graphed(launch, repeats: int = 30, replays: int = 5) -> float:
+    """Average ms of one launch, from a HIP graph of `repeats` launches replayed `replays` times (HIP events around the
+    replays on the capturing stream): the kernel's own time, without the host's launch overhead between eager launches."""
+    import torch
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for _ in range(3):
+            launch()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for _ in range(repeats):
+            launch()
+    torch.cuda.synchronize()
+    begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        graph.replay()
+        begin.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        end.record(stream)
+    torch.cuda.synchronize()
+    return begin.elapsed_time(end) / (repeats * replays)
+
+
 def gemm_case(M: int, K: int, N: int, gated: bool, device, out_dtype=None, epilogue="bias"):
     """config 1: A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02), f32 scales, bias, bf16 (or fp16) out."""
     import torch
@@ -165,12 +191,12 @@ def gemm_bytes(M: int, K: int, N: int, gated: bool, out_bytes: int = 2) -> int:
 
 
 def standalone_gemms(device) -> dict:
-    """the four per-layer shapes at M = 4096, 16384, 65536 with bf16 out."""
+    """the four per-layer shapes at M = 4096, 16384, 65536 with bf16 out, each a graph of 30 launches."""
     import torch
     results = {}
     for M in (4096, 16384, 65536):
         for name, K, N in (("qkv", 512, 1536), ("attention_out", 512, 512), ("ffn_up", 512, 2048), ("ffn_down", 2048, 512)):
-            ms = time_kernel(gemm_case(M, K, N, False, device, torch.bfloat16))
+            ms = time_graphed(gemm_case(M, K, N, False, device, torch.bfloat16))
             tops = 2 * M * N * K / ms / 1e9
             gbs = gemm_bytes(M, K, N, False) / ms / 1e6
             attainable = min(INT8_PEAK_TOPS, 2 * M * N * K / gemm_bytes(M, K, N, False) * HBM_PEAK_GBS / 1e3)
@@ -191,7 +217,7 @@ def standalone_attention(device) -> dict:
     mix[..., torch.arange(H), torch.arange(H)] = 1.0
     templates = (torch.randn(H, 64, 64, device=device, generator=generator) * 0.5).half()
     gains = torch.ones(d, device=device).half()
-    ms = time_kernel(lambda: template_attention(projected, templates, gains, gains, H, H, d, d, H, 1e-5))
+    ms = time_graphed(lambda: template_attention(projected, templates, gains, gains, H, H, d, d, H, 1e-5))
     moved = projected.numel() * 2 + B * T * H * d * 2 + templates.numel() * 2
     return {"ms": round(ms, 4), "gb_per_s": round(moved / ms / 1e6, 1), "frac_of_hbm": round(moved / ms / 1e6 / HBM_PEAK_GBS, 4),
             "bytes": moved, "positions": B}
