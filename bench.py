@@ -206,7 +206,8 @@ def standalone_gemms(device) -> dict:
 
 
 def standalone_attention(device) -> dict:
-    """4096 positions x 8 heads x 64 wide over 64 tokens, a learned 64 x 64 bias per head (one-hot template mix)."""
+    """4096 positions x 8 heads x 64 wide over 64 tokens, a learned 64 x 64 bias per head (one-hot template mix),
+    bf16 Q/K/V and output as the config asks (and the network's fp16 beside it)."""
     import torch
     from model.fused_blocks import template_attention
     B, T, H, d = 4096, 64, 8, 64
@@ -217,10 +218,12 @@ def standalone_attention(device) -> dict:
     mix[..., torch.arange(H), torch.arange(H)] = 1.0
     templates = (torch.randn(H, 64, 64, device=device, generator=generator) * 0.5).half()
     gains = torch.ones(d, device=device).half()
-    ms = time_graphed(lambda: template_attention(projected, templates, gains, gains, H, H, d, d, H, 1e-5))
     moved = projected.numel() * 2 + B * T * H * d * 2 + templates.numel() * 2
-    return {"ms": round(ms, 4), "gb_per_s": round(moved / ms / 1e6, 1), "frac_of_hbm": round(moved / ms / 1e6 / HBM_PEAK_GBS, 4),
-            "bytes": moved, "positions": B}
+    rows_bf16 = projected.bfloat16()
+    ms = time_graphed(lambda: template_attention(rows_bf16, templates, gains, gains, H, H, d, d, H, 1e-5))
+    ms_fp16 = time_graphed(lambda: template_attention(projected, templates, gains, gains, H, H, d, d, H, 1e-5))
+    return {"dtype": "bf16", "ms": round(ms, 4), "gb_per_s": round(moved / ms / 1e6, 1), "frac_of_hbm": round(moved / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "bytes": moved, "positions": B, "fp16_ms": round(ms_fp16, 4)}
 
 
 def gate_up_case(device, batch: int, weight=None, weight_scale=None):

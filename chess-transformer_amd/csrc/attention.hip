@@ -73,10 +73,68 @@ DEVICE void lds_write8(LDS_SPACE void* p, uint2 v) {
     asm volatile("ds_write_b64 %0, %1" : : "v"((uint32_t)(uintptr_t)p), "v"(v) : "memory");
 }
 
-// the sum of squares of 8 halves
-DEVICE float squares8(const v8h& v, float c) {
-    const uint4 w = __builtin_bit_cast(uint4, v);
-    return dot2(w.w, w.w, dot2(w.z, w.z, dot2(w.y, w.y, dot2(w.x, w.x, c))));
+// The rows in and out are fp16, or bf16 (BF16): raw 16-bit values, widened to f32 where they are used. The normalised
+// queries and keys, the template bias and the QK products stay fp16 either way (normalised values are of order one);
+// with bf16 rows P V runs on the bf16 MFMA, P rounded to bf16, and the outputs round to bf16.
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+template <bool BF16> DEVICE float widen16(uint32_t bits) {
+    if constexpr (BF16) return __uint_as_float(bits << 16);
+    else return (float)__builtin_bit_cast(half_t, (uint16_t)bits);
+}
+template <bool BF16> DEVICE uint32_t narrow16(float v) {
+    if constexpr (BF16) return __builtin_bit_cast(uint16_t, (__bf16)v);
+    else return __builtin_bit_cast(uint16_t, (half_t)v);
+}
+// two f32 values rounded to 16 bits, a in the low half: the empty asm keeps them f32 values first, so that a product
+// feeding one is not fused into a mixed-precision multiply-and-round (v_fma_mixlo_f16 rounds the exact product once,
+// not the f32 product); the pair converts in one packed instruction
+typedef __bf16 bf2 __attribute__((ext_vector_type(2)));
+template <bool BF16> DEVICE uint32_t narrow16x2(float a, float b) {
+    asm volatile("" : "+v"(a), "+v"(b));
+    if constexpr (BF16) return __builtin_bit_cast(uint32_t, bf2{(__bf16)a, (__bf16)b});
+    else return __builtin_bit_cast(uint32_t, h2{(half_t)a, (half_t)b});
+}
+// a 16-byte chunk of LDS as raw 16-bit values
+DEVICE uint4 lds_chunk(const LDS_SPACE int8_t* p) {
+    const v4u w = *reinterpret_cast<const LDS_SPACE v4u*>(p);
+    return uint4{w[0], w[1], w[2], w[3]};
+}
+
+// 8 raw values (a 16-byte chunk) as f32
+template <bool BF16> DEVICE void widen8(const uint4& w, float (&out)[8]) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        out[2 * i] = widen16<BF16>(words[i] & 0xFFFFu);
+        out[2 * i + 1] = widen16<BF16>(words[i] >> 16);
+    }
+}
+// 8 bf16 values as fp16 (template coefficients of order one)
+DEVICE uint4 bf16_to_f16x8(const uint4& w) {
+    const uint32_t words[4] = {w.x, w.y, w.z, w.w};
+    uint32_t out[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+        out[i] = narrow16x2<false>(widen16<true>(words[i] & 0xFFFFu), widen16<true>(words[i] >> 16));
+    return uint4{out[0], out[1], out[2], out[3]};
+}
+
+// the sum of squares of 8 raw values: fp16 pairs by v_dot2_f32_f16; bf16 widened, then f32 products in order
+template <bool BF16 = false> DEVICE float squares8(const uint4& w, float c) {
+    if constexpr (BF16) {
+        float v[8];
+        widen8<true>(w, v);
+#pragma unroll
+        for (int i = 0; i < 8; i++) c = __builtin_fmaf(v[i], v[i], c);
+        return c;
+    } else {
+        return dot2(w.w, w.w, dot2(w.z, w.z, dot2(w.y, w.y, dot2(w.x, w.x, c))));
+    }
+}
+// O^T += V^T P^T for one 32-key step: the raw values (fp16 or bf16) and P (already rounded to the same type), 8 a lane
+template <bool BF16> DEVICE v4f pv_step(const uint4& v, const uint4& p, v4f acc) {
+    if constexpr (BF16) return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, v), __builtin_bit_cast(bf8, p), acc, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(v8h, v), __builtin_bit_cast(v8h, p), acc, 0, 0, 0);
 }
 
 // a workgroup's threads: Layout::WAVES wavefronts
@@ -163,7 +221,7 @@ struct DmaPlan {
 // scratch reload would wait for the DMA in flight too); query widths of 128, and value widths of 128 past 96 tokens,
 // spill some. (Fewer registers for more workgroups a CU cost more instructions than they gain: the kernel is bound
 // by its VALU work.)
-template <int DQP, int DV, int TILES, bool SPLIT>
+template <int DQP, int DV, int TILES, bool SPLIT, bool BF16>
 __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__((amdgpu_waves_per_eu(2))) void template_attention_kernel(
     const half_t* __restrict__ projected, const half_t* __restrict__ keyed, const half_t* __restrict__ q_gain,
     const half_t* __restrict__ k_gain, half_t* __restrict__ out, int T, int heads, int kv_heads, int dq, int templates_count,
@@ -311,13 +369,13 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
             const int scale_key = pass * (THREADS / 4) + tid / 4;
             if (KEYS * 4 % THREADS != 0 && scale_key >= KEYS) break;   // a whole wavefront: the last pass's keys are 16 of them
             LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
-            v8h raw[PART_CHUNKS];
+            uint4 raw[PART_CHUNKS];
             float squares = 0.0f;
 #pragma unroll
             for (int c = 0; c < PART_CHUNKS; c++) {
-                raw[c] = *reinterpret_cast<const LDS_SPACE v8h*>(keys + raw_slot<KC>(scale_key, first_chunk + c) * 16);
-                if ((first_chunk + c) * 8 >= dq) raw[c] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-                squares = squares8(raw[c], squares);
+                raw[c] = lds_chunk(keys + raw_slot<KC>(scale_key, first_chunk + c) * 16);
+                if ((first_chunk + c) * 8 >= dq) raw[c] = uint4{0, 0, 0, 0};
+                squares = squares8<BF16>(raw[c], squares);
             }
             squares += lane_xor1(squares);
             squares += lane_xor2(squares);
@@ -325,8 +383,10 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
 #pragma unroll
             for (int c = 0; c < PART_CHUNKS; c++) {
                 v8h normed;
+                float wide[8];
+                widen8<BF16>(raw[c], wide);
 #pragma unroll
-                for (int e = 0; e < 8; e++) normed[e] = (half_t)(((float)raw[c][e] * inverse) * key_gains[c][e]);
+                for (int e = 0; e < 8; e++) normed[e] = (half_t)((wide[e] * inverse) * key_gains[c][e]);
                 *reinterpret_cast<LDS_SPACE v8h*>(keys + raw_slot<KC>(scale_key, first_chunk + c) * 16) = normed;
             }
         }
@@ -352,27 +412,31 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                     coefficients = uint4{c[0] | ((uint32_t)c[1] << 16), c[2] | ((uint32_t)c[3] << 16), c[4] | ((uint32_t)c[5] << 16),
                                          c[6] | ((uint32_t)c[7] << 16)};
                 }
+                if constexpr (BF16) coefficients = bf16_to_f16x8(coefficients);
                 if (!square_query) coefficients = uint4{0, 0, 0, 0};
             }
             // the query row's fragment of B: lane holds dq columns ks * 32 + 8 quad .. + 8
             const LDS_SPACE int8_t* queries = raw_q + (buffer * per_kv + hi) * head_bytes;
             const LDS_SPACE int8_t* keys = raw_k + buffer * L::RAW_K_BYTES;
-            v8h qv[DQP / 32];
+            uint4 qv[DQP / 32];
             float squares = 0.0f;
 #pragma unroll
             for (int ks = 0; ks < DQP / 32; ks++) {
                 const int c = ks * 4 + quad;
-                qv[ks] = *reinterpret_cast<const LDS_SPACE v8h*>(queries + raw_slot<KC>(query, c) * 16);
-                if (c * 8 >= dq) qv[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-                squares = squares8(qv[ks], squares);
+                qv[ks] = lds_chunk(queries + raw_slot<KC>(query, c) * 16);
+                if (c * 8 >= dq) qv[ks] = uint4{0, 0, 0, 0};
+                squares = squares8<BF16>(qv[ks], squares);
             }
             squares = sum_across_rows(squares);
             const float q_inverse = 1.0f / __builtin_sqrtf(squares / columns + eps);
             v8h qf[DQP / 32];
 #pragma unroll
-            for (int ks = 0; ks < DQP / 32; ks++)
+            for (int ks = 0; ks < DQP / 32; ks++) {
+                float wide[8];
+                widen8<BF16>(qv[ks], wide);
 #pragma unroll
-                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)(((float)qv[ks][e] * q_inverse) * gains[ks][e]);
+                for (int e = 0; e < 8; e++) qf[ks][e] = (half_t)((wide[e] * q_inverse) * gains[ks][e]);
+            }
 
             // the bias MFMAs' B operands: this query's coefficients in the one step j with 4 j + quad == col
             v8h mix[4];
@@ -466,12 +530,13 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
             each_step<0, STEPS>([&](auto st_index) {
                 constexpr int st = decltype(st_index)::value, ROW_BYTES = VC * 16;
                 __builtin_amdgcn_sched_barrier(0);
-                v8h pf;
+                uint32_t pw[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    pf[r] = (half_t)s[2 * st][r];
-                    pf[4 + r] = (half_t)s[2 * st + 1][r];
+                for (int r = 0; r < 2; r++) {
+                    pw[r] = narrow16x2<BF16>(s[2 * st][2 * r], s[2 * st][2 * r + 1]);
+                    pw[2 + r] = narrow16x2<BF16>(s[2 * st + 1][2 * r], s[2 * st + 1][2 * r + 1]);
                 }
+                const uint4 pf = uint4{pw[0], pw[1], pw[2], pw[3]};
                 // the step's reads go out together, then one wait for them all
                 v2u halves[DV / 16][2];
 #pragma unroll
@@ -484,12 +549,11 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
                     asm volatile("" : "+v"(halves[dt][0]), "+v"(halves[dt][1]));
-                    const v4h lo = __builtin_bit_cast(v4h, halves[dt][0]), hi = __builtin_bit_cast(v4h, halves[dt][1]);
-                    const v8h vf = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    const uint4 vf = uint4{halves[dt][0][0], halves[dt][0][1], halves[dt][1][0], halves[dt][1][1]};
                     if constexpr (L::BY_STEP && st > 0) {
-                        o[dt] = o[dt] + __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, v4f{0, 0, 0, 0}, 0, 0, 0);
+                        o[dt] = o[dt] + pv_step<BF16>(vf, pf, v4f{0, 0, 0, 0});
                     } else {
-                        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, o[dt], 0, 0, 0);
+                        o[dt] = pv_step<BF16>(vf, pf, o[dt]);
                     }
                 }
             });
@@ -498,17 +562,17 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                 LDS_SPACE int8_t* row = raw_q + (buffer * per_kv + hi) * head_bytes;
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
-                    const v4h result = v4h{(half_t)(o[dt][0] * inverse_total), (half_t)(o[dt][1] * inverse_total),
-                                           (half_t)(o[dt][2] * inverse_total), (half_t)(o[dt][3] * inverse_total)};
-                    lds_write8(row + raw_slot<KC>(query, 2 * dt + quad / 2) * 16 + (quad & 1) * 8, __builtin_bit_cast(uint2, result));
+                    const uint2 result = uint2{narrow16x2<BF16>(o[dt][0] * inverse_total, o[dt][1] * inverse_total),
+                                               narrow16x2<BF16>(o[dt][2] * inverse_total, o[dt][3] * inverse_total)};
+                    lds_write8(row + raw_slot<KC>(query, 2 * dt + quad / 2) * 16 + (quad & 1) * 8, result);
                 }
             } else if (query_ok) {
                 half_t* to = out + (b * T + query) * (heads * DV) + head * DV + quad * 4;
 #pragma unroll
                 for (int dt = 0; dt < DV / 16; dt++) {
-                    const v4h result = v4h{(half_t)(o[dt][0] * inverse_total), (half_t)(o[dt][1] * inverse_total),
-                                           (half_t)(o[dt][2] * inverse_total), (half_t)(o[dt][3] * inverse_total)};
-                    *reinterpret_cast<v4h*>(to + dt * 16) = result;
+                    const uint2 result = uint2{narrow16x2<BF16>(o[dt][0] * inverse_total, o[dt][1] * inverse_total),
+                                               narrow16x2<BF16>(o[dt][2] * inverse_total, o[dt][3] * inverse_total)};
+                    *reinterpret_cast<uint2*>(to + dt * 16) = result;
                 }
             }
 
@@ -521,21 +585,25 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                 const int meta_query = 64 + col;
                 float ms[2][4];
                 if (slab != 2) {
-                    v8h mq[DQP / 32];
+                    uint4 mraw[DQP / 32];
                     float msquares = 0.0f;
 #pragma unroll
                     for (int ks = 0; ks < DQP / 32; ks++) {
                         const int c = ks * 4 + quad;
-                        mq[ks] = *reinterpret_cast<const LDS_SPACE v8h*>(queries + raw_slot<KC>(meta_query, c) * 16);
-                        if (c * 8 >= dq) mq[ks] = v8h{0, 0, 0, 0, 0, 0, 0, 0};
-                        msquares = squares8(mq[ks], msquares);
+                        mraw[ks] = lds_chunk(queries + raw_slot<KC>(meta_query, c) * 16);
+                        if (c * 8 >= dq) mraw[ks] = uint4{0, 0, 0, 0};
+                        msquares = squares8<BF16>(mraw[ks], msquares);
                     }
                     msquares = sum_across_rows(msquares);
                     const float mq_inverse = 1.0f / __builtin_sqrtf(msquares / columns + eps);
+                    v8h mq[DQP / 32];
 #pragma unroll
-                    for (int ks = 0; ks < DQP / 32; ks++)
+                    for (int ks = 0; ks < DQP / 32; ks++) {
+                        float wide[8];
+                        widen8<BF16>(mraw[ks], wide);
 #pragma unroll
-                        for (int e = 0; e < 8; e++) mq[ks][e] = (half_t)(((float)mq[ks][e] * mq_inverse) * gains[ks][e]);
+                        for (int e = 0; e < 8; e++) mq[ks][e] = (half_t)((wide[e] * mq_inverse) * gains[ks][e]);
+                    }
                     float mtop = -__builtin_inff();
 #pragma unroll
                     for (int h2 = 0; h2 < 2; h2++) {
@@ -576,12 +644,13 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                         }
                     mtotal = sum_across_rows(mtotal);
                     if (quad == 0) meta_sum[part * 16 + col] = mtotal;
-                    v8h pf;
+                    uint32_t pw[4];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) {
-                        pf[r] = (half_t)ms[0][r];
-                        pf[4 + r] = (half_t)ms[1][r];
+                    for (int r = 0; r < 2; r++) {
+                        pw[r] = narrow16x2<BF16>(ms[0][2 * r], ms[0][2 * r + 1]);
+                        pw[2 + r] = narrow16x2<BF16>(ms[1][2 * r], ms[1][2 * r + 1]);
                     }
+                    const uint4 pf = uint4{pw[0], pw[1], pw[2], pw[3]};
                     constexpr int ROW_BYTES = VC * 16;
                     const int lo_rows = 32 * part * ROW_BYTES, hi_rows = (32 * part + 16) * ROW_BYTES;
                     const bool has_hi = 32 * part + 16 < L::VKEYS;
@@ -596,9 +665,8 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
 #pragma unroll
                     for (int dt = 0; dt < DV / 16; dt++) {
                         asm volatile("" : "+v"(halves[dt][0]), "+v"(halves[dt][1]));
-                        const v4h lo = __builtin_bit_cast(v4h, halves[dt][0]), hi = __builtin_bit_cast(v4h, halves[dt][1]);
-                        const v8h vf = v8h{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                        const v4f partial = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf, v4f{0, 0, 0, 0}, 0, 0, 0);
+                        const uint4 vf = uint4{halves[dt][0][0], halves[dt][0][1], halves[dt][1][0], halves[dt][1][1]};
+                        const v4f partial = pv_step<BF16>(vf, pf, v4f{0, 0, 0, 0});
                         *reinterpret_cast<v4f*>(mine + dt * 4) = partial;
                     }
                 }
@@ -612,10 +680,10 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
                         const v4f p0 = *reinterpret_cast<const v4f*>(meta_out + lane * (DV / 4) + dt * 4);
                         const v4f p1 = *reinterpret_cast<const v4f*>(meta_out + L::META_OUT + lane * (DV / 4) + dt * 4);
                         const v4f p2 = *reinterpret_cast<const v4f*>(meta_out + 2 * L::META_OUT + lane * (DV / 4) + dt * 4);
-                        v4h result;
+                        float merged[4];
 #pragma unroll
-                        for (int r = 0; r < 4; r++) result[r] = (half_t)(((p0[r] + p1[r]) + p2[r]) * minverse);
-                        *reinterpret_cast<v4h*>(to + dt * 16) = result;
+                        for (int r = 0; r < 4; r++) merged[r] = ((p0[r] + p1[r]) + p2[r]) * minverse;
+                        *reinterpret_cast<uint2*>(to + dt * 16) = uint2{narrow16x2<BF16>(merged[0], merged[1]), narrow16x2<BF16>(merged[2], merged[3])};
                     }
                 }
             }
@@ -628,7 +696,7 @@ __global__ __launch_bounds__((attention_threads<TILES, SPLIT>())) __attribute__(
     }
 }
 
-template <int DQP, int DV, int TILES, bool SPLIT = false>
+template <int DQP, int DV, int TILES, bool SPLIT, bool BF16>
 int launch(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
            int kv_heads, int dq, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
@@ -636,23 +704,24 @@ int launch(const void* projected, const void* keyed, const void* q_gain, const v
     const int bytes = L::bytes(heads / kv_heads);
     if (bytes > 160 * 1024)
         return chess_fail(CHESS_UNSUPPORTED, "template_attention would stage %d bytes of LDS for %d heads a key/value head", bytes, heads / kv_heads);
-    auto kernel = template_attention_kernel<DQP, DV, TILES, SPLIT>;
+    auto kernel = template_attention_kernel<DQP, DV, TILES, SPLIT, BF16>;
     if (bytes > 65536) {
         const hipError_t allowed = hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
         if (allowed != hipSuccess) return (int)allowed;
     }
     const dim3 grid((unsigned)((long)B * kv_heads / groups_per_block)), block(64 * L::WAVES);   // TILES == ceil(T / 16): the caller picked it so
+    // (bf16 rows travel as 16-bit elements behind the same pointers: the kernel reads them only through widen16<BF16>)
     hipLaunchKernelGGL(kernel, grid, block, bytes, stream, (const half_t*)projected, (const half_t*)keyed, (const half_t*)q_gain,
                        (const half_t*)k_gain, (half_t*)out, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale);
     return launch_status();
 }
 
-template <int DQP, int DV>
+template <int DQP, int DV, bool BF16>
 int by_tokens(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
               int kv_heads, int dq, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
     switch ((T + 15) / 16) {
-        case 4: return launch<DQP, DV, 4>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 4: return launch<DQP, DV, 4, false, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
         case 5:
             // four wavefronts a workgroup (the split slab) once the launch has pairs to keep two workgroups on each compute
             // unit busy: at 70 tokens and 8 x 64 heads on an MI355X, each at its best run of pairs a workgroup, batch 1024
@@ -660,31 +729,35 @@ int by_tokens(const void* projected, const void* keyed, const void* q_gain, cons
             // against 21.5. Query and value widths up to 64: past them the split slab's registers spill.
             if constexpr (DQP <= 64 && DV <= 64)
                 if ((long)B * kv_heads >= SPLIT_PAIRS)
-                    return launch<DQP, DV, 5, true>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-            return launch<DQP, DV, 5>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        case 6: return launch<DQP, DV, 6>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        case 7: return launch<DQP, DV, 7>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        default: return launch<DQP, DV, 8>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+                    return launch<DQP, DV, 5, true, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+            return launch<DQP, DV, 5, false, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 6: return launch<DQP, DV, 6, false, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 7: return launch<DQP, DV, 7, false, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        default: return launch<DQP, DV, 8, false, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
     }
 }
 
-template <int DQP>
+template <int DQP, bool BF16>
 int by_dv(const void* projected, const void* keyed, const void* q_gain, const void* k_gain, void* out, int B, int T, int heads,
           int kv_heads, int dq, int dv, int templates_count, int groups_per_block, float eps, float scale, hipStream_t stream)
 {
     switch (dv) {
-        case 16: return by_tokens<DQP, 16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        case 32: return by_tokens<DQP, 32>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        case 64: return by_tokens<DQP, 64>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
-        default: return by_tokens<DQP, 128>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 16: return by_tokens<DQP, 16, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 32: return by_tokens<DQP, 32, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        case 64: return by_tokens<DQP, 64, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
+        default:
+            if constexpr (BF16) return chess_fail(CHESS_UNSUPPORTED, "template_attention takes bf16 rows of value widths up to 64");
+            else return by_tokens<DQP, 128, BF16>(projected, keyed, q_gain, k_gain, out, B, T, heads, kv_heads, dq, templates_count, groups_per_block, eps, scale, stream);
     }
 }
 
 }  // namespace
 
-extern "C" int chess_template_attention(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain, void* out,
-                                        int B, int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block,
-                                        float eps, float scale, void* stream)
+namespace {
+
+template <bool BF16>
+int template_attention(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain, void* out, int B, int T,
+                       int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block, float eps, float scale, void* stream)
 {
     if (B < 0 || T < 64 || T > 128)
         return chess_fail(CHESS_UNSUPPORTED, "template_attention takes 64 to 128 tokens a position, not %d", T);
@@ -692,6 +765,7 @@ extern "C" int chess_template_attention(const void* projected, const void* keyed
         return chess_fail(CHESS_INVALID_SHAPE, "%d heads cannot be split into groups for %d key/value heads", heads, kv_heads);
     if (dq <= 0 || dq > 128 || dq % 8 != 0) return chess_fail(CHESS_UNSUPPORTED, "template_attention takes query widths of 8 to 128 in steps of 8, not %d", dq);
     if (dv != 16 && dv != 32 && dv != 64 && dv != 128) return chess_fail(CHESS_UNSUPPORTED, "template_attention takes value widths 16, 32, 64 or 128, not %d", dv);
+    if (BF16 && (dq > 64 || dv > 64)) return chess_fail(CHESS_UNSUPPORTED, "template_attention takes bf16 rows of query and value widths up to 64, not %d and %d", dq, dv);
     if (templates_count < 0 || templates_count > MAX_TEMPLATES)
         return chess_fail(CHESS_UNSUPPORTED, "template_attention takes at most %d templates, not %d", MAX_TEMPLATES, templates_count);
     if (groups_per_block <= 0 || ((long)B * kv_heads) % groups_per_block != 0)
@@ -702,7 +776,26 @@ extern "C" int chess_template_attention(const void* projected, const void* keyed
         return chess_fail(CHESS_MISALIGNED, "template_attention's vector loads need 16-byte aligned rows (row width %d halves)", width);
     if (B == 0) return CHESS_OK;
     hipStream_t s = (hipStream_t)stream;
-    if (dq <= 32) return by_dv<32>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
-    if (dq <= 64) return by_dv<64>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
-    return by_dv<128>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
+    if (dq <= 32) return by_dv<32, BF16>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
+    if constexpr (!BF16)
+        if (dq > 64) return by_dv<128, BF16>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
+    return by_dv<64, BF16>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count, groups_per_block, eps, scale, s);
+}
+
+}  // namespace
+
+extern "C" int chess_template_attention(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain, void* out,
+                                        int B, int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block,
+                                        float eps, float scale, void* stream)
+{
+    return template_attention<false>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count,
+                                     groups_per_block, eps, scale, stream);
+}
+
+extern "C" int chess_template_attention_bf16(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain,
+                                             void* out, int B, int T, int heads, int kv_heads, int dq, int dv, int templates_count,
+                                             int groups_per_block, float eps, float scale, void* stream)
+{
+    return template_attention<true>(projected, keyed_templates, q_gain, k_gain, out, B, T, heads, kv_heads, dq, dv, templates_count,
+                                    groups_per_block, eps, scale, stream);
 }

@@ -81,9 +81,13 @@ def groups_per_workgroup(positions: int, kv_heads: int, multiprocessors: int = 2
 
 def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, heads: int, kv_heads: int,
                               dq: int, dv: int, templates_count: int, eps: float, groups_per_block: int | None = None) -> torch.Tensor:
+    # rows of fp16 (the network's), or of bf16 (BASELINE's standalone config 2): out in the rows' type; the templates and
+    # gains (parameters) in either, taken as fp16
     for tensor, name in ((projected, "projected"), (templates, "templates"), (q_gain, "q_gain"), (k_gain, "k_gain")):
-        if tensor.dtype != torch.float16:
-            raise ValueError(f"template_attention's {name} is {tensor.dtype}, the kernel takes fp16")
+        if tensor.dtype not in (torch.float16, torch.bfloat16):
+            raise ValueError(f"template_attention's {name} is {tensor.dtype}, the kernel takes fp16 or bf16")
+    bf16 = projected.dtype == torch.bfloat16
+    q_gain, k_gain = q_gain.half(), k_gain.half()
     B, T, width = projected.shape
     if width != heads * dq + kv_heads * dq + kv_heads * dv + heads * templates_count:
         raise ValueError(f"template_attention: rows of {width} are not q | k | v | template mix for {heads} heads, {kv_heads} key/value heads, "
@@ -93,11 +97,11 @@ def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, 
     library = library_for(projected.device)
     projected = aligned(projected)
     keyed = keyed_templates(templates, templates_count)
-    out = torch.empty(B, T, heads * dv, device=projected.device, dtype=torch.float16)
+    out = torch.empty(B, T, heads * dv, device=projected.device, dtype=projected.dtype)
     groups = groups_per_block or groups_per_workgroup(B, kv_heads, torch.cuda.get_device_properties(projected.device).multi_processor_count, T, dq, dv)
-    code = library.chess_template_attention(pointer(projected), pointer(keyed), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()),
-                                            pointer(out), B, T, heads, kv_heads, dq, dv, templates_count, groups, float(eps), 1 / math.sqrt(dq),
-                                            stream_of(projected.device))
+    entry = library.chess_template_attention_bf16 if bf16 else library.chess_template_attention
+    code = entry(pointer(projected), pointer(keyed), pointer(q_gain.contiguous()), pointer(k_gain.contiguous()), pointer(out), B, T, heads,
+                 kv_heads, dq, dv, templates_count, groups, float(eps), 1 / math.sqrt(dq), stream_of(projected.device))
     check(code, "template_attention")
     return out
 

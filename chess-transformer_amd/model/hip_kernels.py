@@ -28,6 +28,7 @@ SIGNATURES = {
     "chess_int8_linear": [_pointer] * 10 + [_int] * 6 + [_pointer],
     "chess_int8_matmul_i32": [_pointer] * 3 + [_int] * 4 + [_pointer],
     "chess_template_attention": [_pointer] * 5 + [_int] * 8 + [_float, _float, _pointer],
+    "chess_template_attention_bf16": [_pointer] * 5 + [_int] * 8 + [_float, _float, _pointer],
     "chess_linear": [_pointer] * 8 + [_int] * 6 + [_pointer],
     "chess_board_embedding": [_pointer, _int] + [_pointer] * 7 + [_int] * 12 + [_pointer],
     "chess_move_logits": [_pointer] * 10 + [ctypes.c_longlong] + [_int] * 8 + [_pointer],

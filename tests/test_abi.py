@@ -74,6 +74,11 @@ def test_refused_shapes_come_back_as_codes(library):
     assert attention(1, 70, 8, 8, 64, 64, 9, 1) == hip_kernels.UNSUPPORTED             # 9 templates
     assert attention(1, 70, 8, 8, 64, 64, 8, 3) == hip_kernels.INVALID_SHAPE           # 3 groups a workgroup for 8
     assert library.chess_template_attention(16, 8, 16, 16, 16, 1, 70, 8, 8, 64, 64, 8, 1, 1e-5, 0.125, None) == hip_kernels.MISALIGNED
+    bf16 = lambda *shape: library.chess_template_attention_bf16(16, 16, 16, 16, 16, *shape, 1e-5, 0.125, None)
+    assert bf16(1, 70, 8, 8, 128, 64, 8, 1) == hip_kernels.UNSUPPORTED               # bf16 rows take widths up to 64
+    assert bf16(1, 70, 8, 8, 64, 128, 8, 1) == hip_kernels.UNSUPPORTED
+    assert bf16(1, 32, 8, 8, 64, 64, 8, 1) == hip_kernels.UNSUPPORTED                # fewer than 64 tokens
+    assert bf16(0, 64, 8, 8, 64, 64, 8, 1) == 0                                      # no positions: nothing to do
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 40, 0, 0, 0, None) == hip_kernels.INVALID_SHAPE
     assert library.chess_linear(16, 16, None, None, None, None, None, 16, 4, 8, 64, 0, 1, 0, None) == hip_kernels.UNSUPPORTED
     moves = lambda *shape, stride=1969, workspace=16, size=1 << 30: library.chess_move_logits(16, 16, 16, 16, 16, 16, 16, 16, 16, workspace, size,

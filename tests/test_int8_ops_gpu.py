@@ -494,10 +494,54 @@ def test_the_split_slab_launch_gives_the_small_launchs_bits(device, heads, kv_he
         assert torch.equal(few, split[rows]), rows
 
 
+def bf16_operands(arguments):
+    projected, templates, *rest = arguments
+    return (projected.bfloat16(), templates, *rest)
+
+
+@pytest.mark.parametrize("heads, kv_heads, dq, dv", [(8, 8, 64, 64), (24, 12, 16, 32), (4, 2, 16, 32)])
+@pytest.mark.parametrize("positions, tokens", [(5, 64), (37, 70), (3, 80)])
+def test_bf16_template_attention_is_the_attention_in_fp32(device, heads, kv_heads, dq, dv, positions, tokens):
+    """bf16 rows in and out (BASELINE config 2's types): the fp32 formula of the reference's test on the same bf16 inputs, at
+    config 2's 1e-2 plus the output's own bf16 rounding; the fp16 kernel's answer on them within 1e-2."""
+    arguments = bf16_operands(attention_operands(device, positions, heads, kv_heads, dq, dv, seed=positions + tokens, tokens=tokens))
+    out = template_attention(*arguments)
+    assert out.dtype == torch.bfloat16
+    expected = reference_attention(arguments)
+    assert ((out.float() - expected).abs() <= 1e-2 + expected.abs() * 2 ** -8).all()
+    halves = template_attention(arguments[0].half(), *arguments[1:])
+    assert (out.float() - halves.float()).abs().max() < 1e-2
+
+
+def test_bf16_template_attention_at_64_tokens_with_a_bias_per_head(device):
+    """BASELINE config 2 in its own types: bf16 Q/K/V and output, a learned 64 x 64 bias per head (one-hot template mix)."""
+    projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps = attention_operands(device, 16, 8, 8, 64, 64, tokens=64)
+    c = projected[..., -heads * count:].reshape(16, 64, heads, count)
+    c.zero_()
+    c[..., torch.arange(heads), torch.arange(heads)] = 1.0
+    arguments = (projected.bfloat16(), templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps)
+    out = template_attention(*arguments)
+    assert out.dtype == torch.bfloat16 and (out.float() - reference_attention(arguments)).abs().max() < 1e-2
+
+
+def test_bf16_split_slab_launch_gives_the_small_launchs_bits(device):
+    """bf16 rows at 70 tokens from 4,096 pairs (the split slab): a position's rows are a three-position launch's bits."""
+    positions = fused_blocks.ATTENTION_SPLIT_PAIRS // 8
+    arguments = bf16_operands(attention_operands(device, positions, 8, 8, 64, 64, seed=70, tokens=70))
+    split = template_attention(*arguments)
+    expected = reference_attention(arguments)
+    # 1e-2 and the output's own bf16 rounding (half an ulp, 2^-9 relative, of the larger of the rounded and exact values)
+    assert ((split.float() - expected).abs() <= 1e-2 + expected.abs() * 2 ** -8).all()
+    for rows in (slice(0, 3), slice(positions - 3, positions)):
+        assert torch.equal(template_attention(arguments[0][rows].contiguous(), *arguments[1:]), split[rows]), rows
+
+
 def test_template_attention_refuses_what_it_cannot_take(device):
     projected, templates, q_gain, k_gain, *rest = attention_operands(device, 2, 8, 8, 64, 64)
     with pytest.raises(ValueError):
         template_attention(projected.float(), templates, q_gain, k_gain, *rest)
+    with pytest.raises(ValueError):   # bf16 rows take query widths up to 64
+        template_attention(*bf16_operands(attention_operands(device, 2, 8, 8, 128, 64)))
     with pytest.raises(ValueError):
         template_attention(projected[:, :, :-8], templates, q_gain, k_gain, *rest)
 
