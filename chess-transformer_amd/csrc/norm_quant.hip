@@ -4,8 +4,9 @@
 //   y = (x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain
 //   absmax = max(max |y|, 1e-20);  q = rint(y * (127 / absmax));  scale = absmax / 127
 // tree_sum is the balanced binary tree of adjacent pairs over the row zero-padded to a power of two.
-// Without the quantisation (QUANT false) the same kernel is the fp16 blocks' RMSNorm: out = f16(y), after the same
-// optional mix (model/fused_blocks.py:346-348 and :351, and the final norm at :863).
+// Without the quantisation (QUANT false) the same kernel is the fp16 blocks' RMSNorm: out = f16(y)
+// (model/fused_blocks.py:348 and :351, and the final norm at :863), after the optional mix as that block writes it in
+// three fp16 ops (:346-347): mixed = f16(f16(x * rs) + f16(original * is)).
 //
 // A row is taken by a group of LANES lanes: the whole wavefront, or 16 lanes for rows up to 512 in large launches, so
 // that a wavefront's instructions serve four rows at once and a row's reductions and divisions are paid once for four. A lane holds J chunks of W contiguous elements
@@ -154,7 +155,14 @@ __global__ __launch_bounds__(64 * WAVES) void norm_quant_kernel(
             half_t m[C];
 #pragma unroll
             for (int i = 0; i < C; i++) {
-                m[i] = (half_t)((v[i] * rs) + (o[i] * is));
+                if constexpr (QUANT) {
+                    m[i] = (half_t)((v[i] * rs) + (o[i] * is));
+                } else {
+                    // each fp16 op rounds: the products (exact in f32) to fp16, then their sum
+                    float scaled = v[i] * rs, added = o[i] * is;
+                    asm volatile("" : "+v"(scaled), "+v"(added));
+                    m[i] = (half_t)((float)(half_t)scaled + (float)(half_t)added);
+                }
                 v[i] = (float)m[i];
             }
             if (live) store_row<C, LANES, VECTOR, FULL>(mixed + base, place, D, m);

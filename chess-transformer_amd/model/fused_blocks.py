@@ -287,7 +287,7 @@ class FusedBlock(nn.Module):
         self.input_mixed = False
 
     def forward(self, x: torch.Tensor, templates: torch.Tensor, original_board_embed: torch.Tensor) -> torch.Tensor:
-        #the input mix, when this block makes it, is (x * rs) + (original * is) rounded once, as the int8 blocks' mix
+        #the input mix, when this block makes it, rounds as the reference's three fp16 ops: f16(f16(rs * x) + f16(is * original))
         if self.input_mixed:
             normed = rms_norm(x, self.ln1.weight, norm_eps(self.ln1, x))
         else:

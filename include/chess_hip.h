@@ -32,9 +32,10 @@ int chess_norm_quant(const void* x, const void* original, const void* residual_s
                      void* mixed, void* q, void* scale, int M, int D, float eps, void* stream);
 
 /* The fp16 blocks' RMSNorm: out[M, D] = f16((x * (1 / sqrt(tree_sum(x * x) / D + eps))) * gain), the f32 order of
- * chess_norm_quant without its quantisation; with original, x is first mixed as there (mixed = f16((x * residual_scale)
- * + (original * input_scale)), written to mixed) and the mixed rows are normalised. Replaces the fp16 block's input mix
- * and ln1 (model/fused_blocks.py:346-348), its ln2 (:351) and the network's final norm (:863), torch's nn.RMSNorm. */
+ * chess_norm_quant without its quantisation; with original, x is first mixed as the fp16 block's three fp16 ops round
+ * it (mixed = f16(f16(x * residual_scale) + f16(original * input_scale)), written to mixed) and the mixed rows are
+ * normalised. Replaces the fp16 block's input mix and ln1 (model/fused_blocks.py:346-348), its ln2 (:351) and the
+ * network's final norm (:863), torch's nn.RMSNorm. */
 int chess_rms_norm(const void* x, const void* original, const void* residual_scale, const void* input_scale, const void* gain, void* mixed,
                    void* out, int M, int D, float eps, void* stream);
 

@@ -96,6 +96,16 @@ def mix(x: np.ndarray, original: np.ndarray, residual_scale, input_scale, dtype=
     return round_to((x.astype(F32) * rs) + (original.astype(F32) * is_), dtype)
 
 
+def mix_in_fp16_steps(x: np.ndarray, original: np.ndarray, residual_scale, input_scale) -> np.ndarray:
+    """The fp16 block's own input mix (model/fused_blocks.py:346-347), three fp16 ops each rounded as torch rounds them:
+    f16(f16(rs * x) + f16(is * original)), each product and the sum formed in f32 (a product of two fp16 is exact there)."""
+    rs = F32(np.asarray(residual_scale, dtype=np.float16).reshape(-1)[0])
+    is_ = F32(np.asarray(input_scale, dtype=np.float16).reshape(-1)[0])
+    scaled = (rs * x.astype(F32)).astype(F16).astype(F32)
+    added = (is_ * original.astype(F32)).astype(F16).astype(F32)
+    return (scaled + added).astype(F16)
+
+
 def norm_quant(x: np.ndarray, gain: np.ndarray, eps: float) -> tuple[np.ndarray, np.ndarray]:
     """model/int8_blocks.py:156-175 (MIX=0): RMSNorm with gain, then per-row int8 and its scale."""
     q, scale = quantize_rows(rms_normalise(x.reshape(-1, x.shape[-1]), gain, eps))
@@ -112,8 +122,8 @@ def mix_norm_quant(x, original, residual_scale, input_scale, gain, eps) -> tuple
 def rms_norm(x: np.ndarray, gain: np.ndarray, eps: float, original=None, residual_scale=None, input_scale=None):
     """The fp16 blocks' RMSNorm (nn.RMSNorm in fp16 at model/fused_blocks.py:348, 351 and 863), in norm_quant's f32 order
     rounded once to fp16: (mixed or None, f16(rms_normalise(mixed or x))). With original, the block's own input mix
-    (:346-347) comes first, as mix() rounds it."""
-    mixed = mix(x, original, residual_scale, input_scale) if original is not None else None
+    (:346-347) comes first, as mix_in_fp16_steps() rounds it."""
+    mixed = mix_in_fp16_steps(x, original, residual_scale, input_scale) if original is not None else None
     rows = mixed if mixed is not None else x
     normed = rms_normalise(rows.reshape(-1, rows.shape[-1]), gain, eps).astype(F16)
     return mixed, normed.reshape(rows.shape)

@@ -288,7 +288,7 @@ def _fp16_block(half: dict, layer: int, x: np.ndarray, templates: np.ndarray, or
     p = f"encoder.{layer}"
     a = lambda name: _np(half, f"{p}.{name}")
     if not input_mixed:
-        x = int8_ops.mix(x, original, a("residual_scale"), a("input_scale"))
+        x = int8_ops.mix_in_fp16_steps(x, original, a("residual_scale"), a("input_scale"))
     norm = lambda v, gain: (_rms(torch.from_numpy(v.astype(np.float64)), torch.from_numpy(gain.astype(np.float64)))).numpy().astype(np.float16)
     projection = np.concatenate([a(f"{n}.weight") for n in ("Q", "K", "V", "template_mix")]).T
     bias = np.concatenate([a(f"{n}.bias") for n in ("Q", "K", "V", "template_mix")])

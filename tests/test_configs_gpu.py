@@ -79,15 +79,19 @@ def check_bars(logits: torch.Tensor, values: torch.Tensor | None, expected_logit
 def test_the_benchmarked_network_meets_the_bars_on_1024_positions(benchmarked):
     """The argmax of a random-init network's policy is often a near tie: two correct CPU restatements of this network (the
     float64 oracle, and the oracle summing its fp16 linear in float32) differ by up to noise["max_logit_difference"]
-    (5.6e-3) in a logit and pick different moves on 3 of the 1,024 positions, whose top two logits are closer than that.
-    So the argmax is held to the bar where the oracle's top two logits are more than twice that apart, and over all
-    positions to no worse than the second restatement's agreement, one position given."""
+    (5.8e-3) in a logit, 5.1e-4 on average, and pick different moves on 4 of the 1,024 positions, whose top two logits
+    are closer than that. So the argmax is held to the bar where the oracle's top two logits are more than twice that
+    apart; the logits on average to within a quarter more than the second restatement's mean difference; and over all
+    positions, where a flip is a near tie's coin toss whose count varies from one correct implementation to another,
+    to no more than twice the second restatement's disagreements and two."""
     data, noise = np.load(FIXTURE), np.load(NOISE)
     boards = torch.from_numpy(data["boards"].astype(np.int64))
     assert torch.equal(boards, legal_boards(len(boards)))
     expected_logits, expected_values = torch.from_numpy(data["logits"]), torch.from_numpy(data["value_logits"])
-    bars = {"decidable_gap": 2 * float(noise["max_logit_difference"]), "least_raw_agreement": float(noise["argmax_agreement"]) - 1 / len(boards)}
+    flips = round((1 - float(noise["argmax_agreement"])) * len(boards))
+    bars = {"decidable_gap": 2 * float(noise["max_logit_difference"]), "least_raw_agreement": 1 - (2 * flips + 2) / len(boards)}
     rows = graphed_rows(benchmarked, boards)
+    assert (rows[:, :-1].double() - expected_logits.double()).abs().mean() <= 1.25 * float(noise["mean_logit_difference"])
     check_bars(rows[:, :-1], None, expected_logits, expected_values, scores=rows[:, -1], **bars)
     benchmarked.fused_heads = False
     try:

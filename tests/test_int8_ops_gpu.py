@@ -63,6 +63,7 @@ def test_rms_norm_matches_the_oracle_to_the_bit(device, rows, D, mix):
         mixed, normed = mix_rms_norm(x, original, rs, is_, gain, 1e-5)
         expected_mixed, expected = oracle.rms_norm(cpu(x), cpu(gain), 1e-5, cpu(original), cpu(rs), cpu(is_))
         assert bits_equal(mixed, expected_mixed)
+        assert torch.equal(mixed, rs * x + is_ * original)   # the reference's fp16 expression, run by torch
         rows_in = mixed
     else:
         normed = rms_norm(x, gain, 1e-5)
