@@ -3,14 +3,16 @@ engine/inference.py (answer_rows, FP16_RESIDUAL_SCALE, fp16_model, int8_model, c
 ImmediateBatches, small_graph_sizes, graph_sizes, chunk_positions), over this build's HIP kernels.
 
 A lane owns a stream, pinned host buffers and one HIP graph per batch size, recorded into a memory pool of its own; a
-batch launches into the smallest graph that holds it on a free lane and is collected later, in any order. A lean lane
-reads board rows that carry the legal moves' answer columns (the native round loop's format) and answers only those
-columns, gathered on the GPU from the answer rows the heads write; its launch and collect go through the HIP runtime's
-entry points by address (engine.hip_runtime), which is how the native loop drives it too. The names of a lane's raw
-handles are the ones that loop reads.
+batch launches into the smallest graph that holds it on a free lane and is collected later, in any order. Whatever the
+lane's kind, a batch goes in by one native call (libchess_hip's chess_lane_submit: the input bytes' copy, the graph, the
+lane's event) and comes out by another (chess_lane_fetch: the answers' copy and the stream's end, the GIL released while
+it waits). A lean lane reads board rows that carry the legal moves' answer columns (the native round loop's format)
+and answers only those columns, gathered on the GPU from the answer rows the heads write; the names of a lane's raw
+handles are the ones the native loop reads, and it drives them through the runtime table of engine.hip_runtime.
 """
 from __future__ import annotations
 
+import bisect
 from collections.abc import Callable
 from pathlib import Path
 
@@ -18,7 +20,7 @@ import numpy as np
 import torch
 from torch import nn
 
-from engine.hip_runtime import DEVICE_TO_HOST, HOST_TO_DEVICE, hip_runtime
+from engine.hip_runtime import HipError
 from model.checkpoint import load_model
 from model.encoding import NUM_MOVE_IDS, START_POSITION_TOKENS, TOKENS_PER_BOARD
 from model.hip_kernels import check, library_for, pointer, stream_of
@@ -169,81 +171,104 @@ clear_cublas_workspaces = clear_blas_workspaces
 
 
 class Lane:
-    """One batch in flight at a time: a stream, pinned host buffers, and a graph per size recorded in a pool of its own
-    (lanes sharing a pool would write over each other's activations). A lean lane's boards come as LEAN_ROW-byte rows
-    (rows_array, filled by the caller) and its answers are LEAN_COLUMNS floats a board. warm_up runs the model once per
-    size before recording (a network's later lanes skip it)."""
+    """One batch in flight at a time, on a stream of the lane's own. Its memory: the input its graphs read -- a lean lane's
+    LEAN_ROW-byte board rows, another lane's int64 board tokens -- with a pinned host twin that the caller fills
+    (rows_array or boards_array); one answers tensor a batch size, which that size's graph writes; and a pinned answers
+    buffer. The graphs are recorded largest first into a pool of the lane's own (two lanes in one pool would write over
+    each other's activations), after a warm-up forward a size on the lane's stream when warm_up is set (a network's later
+    lanes skip it). A batch goes in and comes out by one native call each, chess_lane_submit and chess_lane_fetch, on
+    the raw handles that handles() also gives the native round loop: the lane moves bytes, not tensors."""
 
     def __init__(self, model: nn.Module, sizes: list[int], chunk: int | None, lean: bool = False, warm_up: bool = True):
         self.lean, self.chunk = lean, chunk
+        self.pending = False          # launched and not collected: a second launch would overwrite its answers
         self.device = torch.cuda.current_device()
         self.stream = torch.cuda.Stream()
         self.done = torch.cuda.Event(blocking=True)
-        # launched and not collected yet: another launch would overwrite its answers
-        self.pending = False
-        self._buffers(sizes[-1])
-        self._record(model, sizes, warm_up)
+        self.library = library_for(torch.device("cuda", self.device))
+        self._allocate(max(sizes))
+        self.graphs, self.answers = self._record(model, sorted(sizes, reverse=True), warm_up)
+        self.executables = {size: graph.raw_cuda_graph_exec() for size, graph in self.graphs.items()}
 
-    def _buffers(self, largest: int) -> None:
-        # the graphs record on a real position, the start position's tokens in every row
-        self.boards = torch.tensor(START_POSITION_TOKENS, dtype=torch.long, device="cuda").expand(largest, -1).contiguous()
-        width = LEAN_COLUMNS if self.lean else ANSWER_WIDTH
-        self.answers_host = torch.zeros(largest, width, dtype=torch.float32, pin_memory=True)
-        self.answers_array = self.answers_host.numpy()
+    def _allocate(self, largest: int) -> None:
+        # the graphs record on the start position in every row: real tokens, so every kernel sees a board it can take
+        self.boards = torch.tensor(START_POSITION_TOKENS, dtype=torch.long, device="cuda").repeat(largest, 1)
         if self.lean:
             self.rows = torch.empty(largest, LEAN_ROW, dtype=torch.uint8, device="cuda")
             self.rows[:, :TOKENS_PER_BOARD] = self.boards
-            # every column the expected score's until a launch brings real rows
+            # until a launch brings real rows, every column is the expected score's
             self.rows[:, TOKENS_PER_BOARD:].view(torch.int16).fill_(ANSWER_WIDTH - 1)
             self.rows_host = torch.zeros(largest, LEAN_ROW, dtype=torch.uint8, pin_memory=True)
+            self.input, self.input_host = self.rows, self.rows_host
             self.rows_array = self.rows_host.numpy()
         else:
             self.boards_host = torch.zeros(largest, TOKENS_PER_BOARD, dtype=torch.long, pin_memory=True)
+            self.input, self.input_host = self.boards, self.boards_host
             self.boards_array = self.boards_host.numpy()
+        self.answer_width = LEAN_COLUMNS if self.lean else ANSWER_WIDTH
+        self.answers_host = torch.zeros(largest, self.answer_width, dtype=torch.float32, pin_memory=True)
+        self.answers_array = self.answers_host.numpy()
 
     def answer(self, model: nn.Module, size: int, chunk: int | None = None) -> torch.Tensor:
-        """The forward a graph records: the first size boards (a lean lane's taken from its rows) to answers."""
+        """The forward a graph records: the first size boards (a lean lane's taken from its rows) to their answers."""
         chunk = self.chunk if chunk is None else chunk
         if not self.lean:
             return chunked_answer_rows(model, self.boards[:size], chunk)
         self.boards[:size].copy_(self.rows[:size, :TOKENS_PER_BOARD])
         return chunked_lean_rows(model, self.boards[:size], self.rows[:size], chunk)
 
-    def _record(self, model: nn.Module, sizes: list[int], warm_up: bool) -> None:
-        # graphs record after warm-up calls made off the default stream
+    def _record(self, model: nn.Module, sizes: list[int], warm_up: bool) -> tuple[dict, dict]:
         self.stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(self.stream), torch.no_grad():
             for size in sizes if warm_up else ():
                 self.answer(model, size)
         torch.cuda.current_stream().wait_stream(self.stream)
         self.pool = torch.cuda.graph_pool_handle()
-        self.graphs, self.answers = {}, {}
-        for size in sorted(sizes, reverse=True):      # the largest first: it sizes the pool the smaller ones reuse
-            graph = torch.cuda.CUDAGraph()
+        graphs, answers = {}, {}
+        for size in sizes:
+            graphs[size] = torch.cuda.CUDAGraph()
             clear_blas_workspaces()
-            with torch.cuda.graph(graph, pool=self.pool, stream=self.stream), torch.no_grad():
-                self.answers[size] = self.answer(model, size)
+            with torch.cuda.graph(graphs[size], pool=self.pool, stream=self.stream), torch.no_grad():
+                answers[size] = self.answer(model, size)
             clear_blas_workspaces()
-            self.graphs[size] = graph
-        # the event gets its handle at its first record
+        # the event has a handle once recorded
         self.done.record(self.stream)
         self.done.synchronize()
-        if self.lean and not all(answers.dtype == torch.float32 and answers.is_contiguous() for answers in self.answers.values()):
-            raise RuntimeError("a lean lane's collect copies its answers' bytes: they must be contiguous f32")
+        for size, rows in answers.items():
+            if rows.dtype != torch.float32 or not rows.is_contiguous() or tuple(rows.shape) != (size, self.answer_width):
+                raise RuntimeError(f"a lane copies its answers' bytes: {size} x {self.answer_width} contiguous f32, not {tuple(rows.shape)} "
+                                   f"{rows.dtype}")
+        return graphs, answers
+
+    def _check(self, code: int) -> None:
+        if code:
+            raise HipError(self.library.chess_last_error().decode())
+
+    def submit(self, count: int, size: int) -> None:
+        """The first count boards of the host input in, and size's graph started behind them."""
+        row_bytes = self.input.shape[1] * self.input.element_size()
+        self._check(self.library.chess_lane_submit(self.device, self.stream.cuda_stream, self.input.data_ptr(), self.input_host.data_ptr(),
+                                                   count * row_bytes, self.executables[size], self.done.cuda_event))
+
+    def fetch(self, count: int, size: int, sleep: bool) -> np.ndarray:
+        """The batch's count answer rows, in the pinned buffer, once size's graph is done (slept on when sleep)."""
+        self._check(self.library.chess_lane_fetch(self.device, self.stream.cuda_stream, self.done.cuda_event, int(sleep),
+                                                  self.answers_host.data_ptr(), self.answers[size].data_ptr(), count * self.answer_width * 4))
+        return self.answers_array[:count]
 
     def handles(self) -> dict:
-        """The raw handles a lean launch and collect (and the native round loop) pass to the HIP runtime; graphs maps a size to
-        (its executable graph, its answers on the device)."""
+        """The raw handles for the native round loop: graphs maps a size to (its executable graph, its answers on the device)."""
         return {"device": self.device, "stream": self.stream.cuda_stream, "done": self.done.cuda_event, "rows_host": self.rows_host.data_ptr(),
                 "rows": self.rows.data_ptr(), "answers_host": self.answers_host.data_ptr(),
-                "graphs": {size: (graph.raw_cuda_graph_exec(), self.answers[size].data_ptr()) for size, graph in self.graphs.items()}}
+                "graphs": {size: (self.executables[size], self.answers[size].data_ptr()) for size in self.graphs}}
 
 
 class GraphedBatches:
-    """The model as graphs on in_flight lanes (reference :145-226): launch returns at once, collect waits; batches may be
-    collected in any order, at most in_flight out at a time. A batch takes the smallest graph that holds it on the first
-    free lane. chunk: boards a forward (chunk_positions; None, a batch's all at once). blocking_wait: collect sleeps on
-    an event rather than spinning a core. lean: lean lanes, filled by the caller (rows_array) and run by launch_filled."""
+    """The model as graphs on in_flight lanes (the reference's interface, engine/inference.py:145-226): launch returns at
+    once and collect waits, in any order, with at most in_flight batches out. A batch takes the smallest graph that holds
+    it, on the first free lane. chunk: boards a forward (chunk_positions; None, a batch's all at once). blocking_wait:
+    collect sleeps on the lane's event rather than spinning a core. lean: lean lanes, whose rows_array the caller fills
+    before launch_filled."""
 
     def __init__(self, model: nn.Module, sizes: list[int], in_flight: int = 2, chunk: int | None = None, blocking_wait: bool = False,
                  lean: bool = False):
@@ -251,21 +276,20 @@ class GraphedBatches:
         self.sizes = sorted(sizes)
         self.lean, self.blocking_wait = lean, blocking_wait
         self.lanes = [Lane(model, self.sizes, chunk, lean, warm_up=index == 0) for index in range(in_flight)]
-        self.runtime = hip_runtime() if lean else None
         self.handles = {id(lane): lane.handles() for lane in self.lanes} if lean else {}
 
     def free_lane(self) -> Lane:
         """The lane the next launch takes; the caller may fill its boards_array (a lean lane's rows_array) for launch_filled."""
-        for lane in self.lanes:
-            if not lane.pending:
-                return lane
-        raise RuntimeError("more batches in flight than lanes")
+        free = [lane for lane in self.lanes if not lane.pending]
+        if not free:
+            raise RuntimeError("more batches in flight than lanes")
+        return free[0]
 
     def _size_for(self, count: int) -> int:
-        for size in self.sizes:
-            if size >= count:
-                return size
-        raise ValueError(f"{count} boards are more than the largest graph's {self.sizes[-1]}")
+        index = bisect.bisect_left(self.sizes, count)
+        if index == len(self.sizes):
+            raise ValueError(f"{count} boards are more than the largest graph's {self.sizes[-1]}")
+        return self.sizes[index]
 
     def launch(self, boards: np.ndarray) -> tuple[Lane, int, int]:
         if self.lean:
@@ -275,44 +299,19 @@ class GraphedBatches:
         return self.launch_filled(lane, len(boards))
 
     def launch_filled(self, lane: Lane, count: int) -> tuple[Lane, int, int]:
-        """Starts the lane's first count boards. A lean lane's runtime calls leave the thread's current device at the lane's."""
+        """Starts the lane's first count boards; leaves the thread's current device at the lane's."""
         size = self._size_for(count)
+        lane.submit(count, size)
         lane.pending = True
-        if lane.lean:
-            runtime, handles = self.runtime, self.handles[id(lane)]
-            stream = handles["stream"]
-            runtime.check(runtime.set_device(handles["device"]), "the lane's device")
-            runtime.check(runtime.memcpy(handles["rows"], handles["rows_host"], count * LEAN_ROW, HOST_TO_DEVICE, stream), "the boards' copy")
-            runtime.check(runtime.graph_launch(handles["graphs"][size][0], stream), "the graph's launch")
-            runtime.check(runtime.event_record(handles["done"], stream), "the batch's event")
-        else:
-            with torch.cuda.stream(lane.stream):
-                lane.boards[:count].copy_(lane.boards_host[:count], non_blocking=True)
-                lane.graphs[size].replay()
-                if self.blocking_wait:
-                    lane.done.record(lane.stream)
         return lane, size, count
 
     def collect(self, launched: tuple[Lane, int, int]) -> np.ndarray:
         """The batch's answers, in the lane's pinned buffer. They are copied back here rather than at launch: the GPU's copies
         queue, and one made at launch would hold the other lane's boards behind this batch's forward."""
         lane, size, count = launched
-        if lane.lean:
-            runtime, handles = self.runtime, self.handles[id(lane)]
-            stream = handles["stream"]
-            runtime.check(runtime.set_device(handles["device"]), "the lane's device")
-            if self.blocking_wait:
-                runtime.check(runtime.event_synchronize(handles["done"]), "the batch")
-            answers = handles["graphs"][size][1]
-            runtime.check(runtime.memcpy(handles["answers_host"], answers, count * LEAN_COLUMNS * 4, DEVICE_TO_HOST, stream), "the answers' copy")
-            runtime.check(runtime.stream_synchronize(stream), "the batch")
-        else:
-            if self.blocking_wait:
-                lane.done.synchronize()
-            with torch.cuda.stream(lane.stream):
-                lane.answers_host[:count].copy_(lane.answers[size][:count])
+        answers = lane.fetch(count, size, self.blocking_wait)
         lane.pending = False
-        return lane.answers_array[:count]
+        return answers
 
     def rust_network(self) -> dict:
         """What the native round loop holds: the lean lanes' handles (it keeps this object, so every lane lives while it runs)."""

@@ -36,11 +36,15 @@ SIGNATURES = {
     "chess_value_head_no_alloc": [_pointer] * 8 + [_int] * 6 + [_pointer],
     "chess_lean_answers": [_pointer] * 3 + [_int] * 5 + [_pointer],
     "chess_runtime_addresses": [ctypes.POINTER(ctypes.c_void_p), _int],
+    "chess_lane_submit": [_int] + [_pointer] * 3 + [ctypes.c_size_t] + [_pointer] * 2,
+    "chess_lane_fetch": [_int] + [_pointer] * 2 + [_int] + [_pointer] * 2 + [ctypes.c_size_t],
     "chess_error_string": [_int],
     "chess_last_error": [],
     "chess_target": [],
 }
 STRINGS = ("chess_error_string", "chess_last_error", "chess_target")
+# calls that wait for the GPU: bound through CDLL, which releases the GIL for the call, so other threads run meanwhile
+WAITS = ("chess_lane_fetch",)
 
 _lock = threading.Lock()
 _library: ctypes.CDLL | None = None
@@ -57,10 +61,12 @@ def load_library(path: Path = LIBRARY_PATH) -> ctypes.CDLL:
             # PyDLL: a launch only queues work, so it keeps the GIL and skips releasing it (as the reference's
             # quick runtime calls do, engine/cuda_runtime.py:16, 33)
             library = ctypes.PyDLL(str(path))
+            waiting = ctypes.CDLL(str(path))
             for name, arguments in SIGNATURES.items():
-                function = getattr(library, name)
+                function = getattr(waiting if name in WAITS else library, name)
                 function.argtypes = arguments
                 function.restype = ctypes.c_char_p if name in STRINGS else ctypes.c_int
+                setattr(library, name, function)
             _library = library
         return _library
 

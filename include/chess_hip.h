@@ -12,6 +12,8 @@
 #ifndef CHESS_HIP_H
 #define CHESS_HIP_H
 
+#include <stddef.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -147,6 +149,17 @@ int chess_lean_answers(const void* answer_rows, const void* rows, void* answers,
  * and addresses()), whose HIP functions have the CUDA ones' signatures; the native round loop
  * (engine/selfplay_rs/src/rounds.rs:19-56) calls them by address. */
 int chess_runtime_addresses(void** table, int count);
+
+/* A graph lane's batch in: with `device` current, bytes of input copied from pinned input_host to input on stream, the
+ * recorded graph (a hipGraphExec_t) launched on stream, and the event done recorded behind it. The four runtime calls
+ * that the reference's GraphedBatches.launch_filled makes one at a time (engine/inference.py:183-195). A failed step
+ * returns its HIP error, and chess_last_error names the step. */
+int chess_lane_submit(int device, void* stream, void* input, const void* input_host, size_t bytes, void* graph, void* done);
+
+/* A graph lane's batch out: with `device` current, a wait on done when sleep is non-zero, then bytes of output copied
+ * to pinned output_host on stream and the stream awaited: GraphedBatches.collect (engine/inference.py:199-214). It
+ * blocks; Python binds it so that it releases the GIL while it waits. */
+int chess_lane_fetch(int device, void* stream, void* done, int sleep, void* output_host, const void* output, size_t bytes);
 
 /* A description of a code, and the message of the last refused call on this thread. */
 const char* chess_error_string(int code);

@@ -38,9 +38,10 @@ def test_the_loaders_argument_types_are_the_headers(library):
         for argument in arguments:
             kind = argument.rsplit(" ", 1)[0] if " " in argument else argument
             expected.append(ctypes.c_void_p if "*" in argument else ctypes.c_float if kind.endswith("float")
-                            else ctypes.c_longlong if kind.endswith("long long") else ctypes.c_int)
+                            else ctypes.c_longlong if kind.endswith("long long") else ctypes.c_size_t if kind.endswith("size_t")
+                            else ctypes.c_int)
         declared = hip_kernels.SIGNATURES[name]
-        normalised = [t if t in (ctypes.c_int, ctypes.c_float, ctypes.c_longlong) else ctypes.c_void_p for t in declared]
+        normalised = [t if t in (ctypes.c_int, ctypes.c_float, ctypes.c_longlong, ctypes.c_size_t) else ctypes.c_void_p for t in declared]
         assert normalised == expected, name
 
 
@@ -124,6 +125,15 @@ def test_codes_become_value_errors_with_the_message(library):
         hip_kernels.check(hip_kernels.INVALID_SHAPE, "rotate_quant")
     with pytest.raises(RuntimeError, match="HIP error"):
         hip_kernels.check(1, "launch")
+
+
+def test_lane_calls_refuse_missing_handles_before_touching_a_device(library):
+    assert library.chess_lane_submit(0, None, 16, 16, 64, 16, 16) == hip_kernels.INVALID_SHAPE
+    assert b"lane_submit" in library.chess_last_error()
+    assert library.chess_lane_submit(0, 16, None, 16, 64, 16, 16) == hip_kernels.INVALID_SHAPE
+    assert library.chess_lane_fetch(0, 16, None, 1, 16, 16, 64) == hip_kernels.INVALID_SHAPE
+    assert library.chess_lane_fetch(0, 16, 16, 0, None, 16, 64) == hip_kernels.INVALID_SHAPE
+    assert b"lane_fetch" in library.chess_last_error()
 
 
 def test_the_runtime_table_has_the_reference_calls(library):
