@@ -358,7 +358,7 @@ def test_the_config1_gemms_are_the_oracles_in_bf16(device, M, K, N):
     assert np.array_equal(cpu(out.float())[rows], expected)
 
 
-ALL_TILES = tuple(range(1, 14))   # 12 and 13 take 128-byte stages
+ALL_TILES = tuple(range(1, 14))   # 12 and 13 take 128-byte stages, 4 eight wavefronts
 SPLIT_TILES = (14,)              # int8 only
 
 
