@@ -14,14 +14,15 @@
 // from one position into the next; it has one wavefront per slab of 16 queries, or (SPLIT, five slabs in large
 // launches) four wavefronts, three of which share the fifth slab by 32-key step. A group's raw key, value and
 // query rows arrive by DMA into LDS, double-buffered: the next group's rows load while this group's heads run.
-// A wavefront then runs each head of the group on v_mfma_f32_16x16x32_f16: the scores come out transposed,
-// S^T = K Q^T, from the raw keys and a per-key scale, so a lane holds one query's scores for 4 keys of each
-// 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B operand, so the probabilities never leave
-// registers. V^T's fragments are read from the raw value rows by transposing LDS reads (ds_read_b64_tr_b16: in
+// The keys are normalised in place in LDS (four threads a key), the queries in registers; a wavefront then runs
+// each head of the group on v_mfma_f32_16x16x32_f16: the scores come out transposed, S^T = K' Q'^T, so a lane
+// holds one query's scores for 4 keys of each 16-key tile -- exactly the fragment O^T = V^T P^T needs as its B
+// operand, so the probabilities never leave registers. V^T's fragments are read from the raw value rows by transposing LDS reads (ds_read_b64_tr_b16: in
 // each 16 lanes, lane j receives element j % 4 of the 8 bytes lanes j / 4 + 4 r address, r = 0..3), so the
 // values are never transposed in LDS. The template bias is an MFMA too, from the templates held in registers.
-// Attention is held to a tolerance, not to bits: the norms take the hardware reciprocal square root, sums
-// of squares are v_dot2_f32_f16 of the fp16 pairs, and the softmax's exponent is one fma.
+// Attention is held to a tolerance, not to bits: its f32 sums run in the MFMA's and the lanes' order (sums of
+// squares are v_dot2_f32_f16 of the fp16 pairs), the norms take IEEE divides and square roots, and the softmax's
+// exponent is one fma into the hardware exp2.
 #include "chess_common.h"
 
 #include <type_traits>
