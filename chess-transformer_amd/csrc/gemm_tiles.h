@@ -486,16 +486,20 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
     }
 }
 
-// The tile for tile 0: large launches take the 2-stage 128 x 128, with 128-byte stages for rows of 2 KB or more that
-// are a multiple of 128 bytes (each L2 line of an operand row read once); launches that still give the chip a 128 x 128
-// workgroup a compute unit take 128-byte stages for any row of a multiple of 128 bytes, smaller ones the 128 x 64 tiles
-// (128-byte stages where the rows allow), the smallest 64 x 64. Timed on an MI355X (int8, bf16 out, graphs of 30
-// launches): M = 16,384 by 512 -> 512 in 11.7 against 12.6 us and 2,048 -> 512 in 25.1 against 29.0 (tile 2); M = 4,096
-// by 2,048 -> 512 in 10.3 against 10.5 (tile 3).
+// The tile for tile 0: int8 launches of 32,768 rows or more take the eight-wavefront 256 x 128; other large launches the
+// 2-stage 128 x 128, with 128-byte stages for rows of 2 KB or more that are a multiple of 128 bytes (each L2 line of an
+// operand row read once); launches that still give the chip a 128 x 128 workgroup a compute unit take 128-byte stages
+// for any row of a multiple of 128 bytes, smaller ones the 128 x 64 tiles (128-byte stages where the rows allow), the
+// smallest 64 x 64. Timed on an MI355X (int8, bf16 out, bias, graphs of 30 launches): M = 65,536 by 512 -> 2,048 in
+// 124.7 against 127.6 us (tile 11), 2,048 -> 512 in 84.6 against 89.6 (tile 13), 512 -> 1,536 in 94.5 against 96.2;
+// M = 16,384 by 512 -> 512 in 11.7 against 12.6 us and 2,048 -> 512 in 25.1 against 29.0 (tile 2); M = 4,096 by
+// 2,048 -> 512 in 10.3 against 10.5 (tile 3).
 template <typename In> int tile_by_size(int M, int N, int K) {
     const size_t row_bytes = (size_t)K * sizeof(In);
     const bool whole_lines = row_bytes % 128 == 0;
-    if ((long)((M + 255) / 256) * ((N + 127) / 128) >= 512) return row_bytes >= 2048 && whole_lines ? 13 : 11;
+    const bool big = (long)((M + 255) / 256) * ((N + 127) / 128) >= 512;
+    if (big && sizeof(In) == 1 && M >= 32768) return 4;
+    if (big) return row_bytes >= 2048 && whole_lines ? 13 : 11;
     if ((long)((M + 127) / 128) * ((N + 127) / 128) >= 256) return whole_lines ? 13 : 2;
     if ((long)((M + 127) / 128) * ((N + 63) / 64) >= 128) return whole_lines ? 12 : 3;
     return 1;
