@@ -23,9 +23,10 @@ from model.model import EDGE, KING, KNIGHT, NO_PIECE, PAWN, QUEEN, THEIRS, Chess
 LINEAR_DEPTH, GROUP_M = 32, 8
 FEATURE_SLOTS = 23
 # linear's tiles by the rows a compute unit's share is (reference fused_blocks.py:183-185), the GEMM's tile numbers: tiles
-# 1, 3 and 8 keep the small batches' launches on more compute units than tile 11's 128 x 128 (the network at batch 16 / 32
-# / 64: 0.16 / 0.11 / 0.03 ms a forward faster)
-LINEAR_TILES = {"gfx950": [(5, 1), (9, 3), (18, 8), (math.inf, 11)]}
+# 1 and 3 keep the small batches' launches on more compute units than tile 11's 128 x 128 (the network at batch 16 / 32:
+# 0.16 / 0.11 ms a forward faster), and from 9 to 48 rows the eight-wavefront 128 x 128 tile 6 (the network, alternated
+# on one box: batch 64 2.455-2.468 against 2.506-2.510 ms a forward with tile 8, batch 128 3.82-3.85 against 3.86 with 11)
+LINEAR_TILES = {"gfx950": [(5, 1), (9, 3), (48, 6), (math.inf, 11)]}
 # f32 out (accumulate_fp32, the policy head's `a`): its f32 staging runs faster at 128 x 128 with a 3-stage ring (78 against
 # 97 us at 71,680 rows on an MI355X)
 LINEAR_F32_TILES = {"gfx950": [(4, 1), (math.inf, 7)]}
