@@ -30,7 +30,7 @@
 namespace {
 
 constexpr int MAX_TEMPLATES = 8;
-constexpr long SPLIT_PAIRS = 4096;   // (position, key/value group) pairs from which a 65-80 token launch takes the split slab
+constexpr long SPLIT_PAIRS = 2048;   // (position, key/value group) pairs from which a 65-80 token launch takes the split slab
 constexpr float LOG2E = 1.44269504f;
 
 typedef __fp16 h2 __attribute__((ext_vector_type(2)));
