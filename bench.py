@@ -1,7 +1,7 @@
 """Benchmark of Fry's int8 network evaluation on one MI355X.
 
 A step is one forward of the 28-block d512 int8 network (27 int8 blocks + the fp16 last, the reference's semantics at
-BASELINE's sizes) over a batch of synthetic positions already on the GPU, replayed as a HIP graph as the engine's lanes
+the benchmark's sizes) over a batch of synthetic positions already on the GPU, replayed as a HIP graph as the engine's lanes
 replay theirs. Prints ONE JSON line: positions/s at batch 1024 (value), batch-64 latency, the standalone GEMM and
 attention configs, the roofline of the dominant kernel (timed with HIP events on the stream it runs on) and the CPU
 baseline (the CPU oracle's fp32 forward, the reference's CPU path, on a bounded sample, on this host's cores).
@@ -49,7 +49,7 @@ def log(message: str) -> None:
 
 
 def synthetic_model(settings: dict, seed: int = 0):
-    """Random-init weights as BASELINE states them: linear weights and biases N(0, 0.02), norm gains 1 + N(0, 0.1), templates
+    """Random-init weights as the benchmark states them: linear weights and biases N(0, 0.02), norm gains 1 + N(0, 0.1), templates
     N(0, 0.5), square-feature table N(0, 0.1), the input mixed in (residual 0.8, input 0.5). Drawn with numpy's generator
     (PCG64, float32 normals), whose stream is the same on every machine, so that the GPU box builds the very network the
     committed expected outputs (tests/golden/) were computed for."""
@@ -191,7 +191,7 @@ def gemm_bytes(M: int, K: int, N: int, gated: bool, out_bytes: int = 2) -> int:
 
 
 def standalone_gemms(device) -> dict:
-    """the four per-layer shapes at M = 4096, 16384, 65536 with bf16 out, each a graph of 30 launches."""
+    """benchmark config 1: the four per-layer shapes at M = 4096, 16384, 65536 with bf16 out, each a graph of 30 launches."""
     import torch
     results = {}
     for M in (4096, 16384, 65536):
@@ -206,7 +206,7 @@ def standalone_gemms(device) -> dict:
 
 
 def standalone_attention(device) -> dict:
-    """4096 positions x 8 heads x 64 wide over 64 tokens, a learned 64 x 64 bias per head (one-hot template mix),
+    """benchmark config 2: 4096 positions x 8 heads x 64 wide over 64 tokens, a learned 64 x 64 bias per head (one-hot template mix),
     bf16 Q/K/V and output as the config asks (and the network's fp16 beside it)."""
     import torch
     from model.fused_blocks import template_attention
@@ -540,7 +540,7 @@ def time_cpu_forward(state: dict, settings: dict, batch: int, threads: int, runs
 
 
 def cpu_baseline(model_state: dict, runs: int = 20, warmups: int = 3) -> dict:
-    """The CPU baseline of BASELINE.md's protocol: the fp32 CPU forward of config 0 (d256 x 4, batch 64) and config 3 (the d512 x
+    """The CPU baseline: the fp32 CPU forward of config 0 (d256 x 4, batch 64) and config 3 (the d512 x
     28 network, batch 64), p50 and p99 over runs after warmups, on every CPU this process may use and on one thread (the
     engine's own setting, reference engine/uci.py:557). The one-thread d512 x 28 figure takes batches of 8 (a forward of 64
     takes about 15 s on one core), still 20 runs. value: config 3 on all usable threads, positions/s at the p50."""

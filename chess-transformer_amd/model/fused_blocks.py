@@ -83,7 +83,7 @@ def groups_per_workgroup(positions: int, kv_heads: int, multiprocessors: int = 2
 
 def launch_template_attention(projected: torch.Tensor, templates: torch.Tensor, q_gain: torch.Tensor, k_gain: torch.Tensor, heads: int, kv_heads: int,
                               dq: int, dv: int, templates_count: int, eps: float, groups_per_block: int | None = None) -> torch.Tensor:
-    # rows of fp16 (the network's), or of bf16 (BASELINE's standalone config 2): out in the rows' type; the templates and
+    # rows of fp16 (the network's), or of bf16 (the benchmark's standalone config 2): out in the rows' type; the templates and
     # gains (parameters) in either, taken as fp16
     for tensor, name in ((projected, "projected"), (templates, "templates"), (q_gain, "q_gain"), (k_gain, "k_gain")):
         if tensor.dtype not in (torch.float16, torch.bfloat16):

@@ -77,7 +77,7 @@ int chess_template_attention(const void* projected, const void* keyed_templates,
 /* chess_template_attention with projected and out in bf16 (query and value widths up to 64): the same arguments,
  * keyed_templates and the gains still fp16. The normalised queries and keys, the template bias and the scores stay
  * fp16 as in the fp16 entry point; P V runs on the bf16 MFMA with P rounded to bf16.
- * No counterpart in the reference, whose attention is fp16 only (model/attention_cuda.py:97-304)
+ * No counterpart in the reference, whose attention is fp16 only (model/attention_cuda.py:97-304): the benchmark's config 2
  * (4,096 positions x 8 heads x 64, 64 tokens) asks for bf16 Q/K/V and a bf16 output. */
 int chess_template_attention_bf16(const void* projected, const void* keyed_templates, const void* q_gain, const void* k_gain, void* out,
                                   int B, int T, int heads, int kv_heads, int dq, int dv, int templates_count, int groups_per_block,

@@ -1,5 +1,5 @@
 """Writes tests/golden/positions.npz: 4,096 seeded random legal positions as the network's tokens (uint8 [4096, 70]) and the
-plies each took, for BASELINE's configs 0, 3 and 4 (positions reached by 0-80 uniformly random legal moves from the start
+plies each took, for the benchmark's configs 0, 3 and 4 (positions reached by 0-80 uniformly random legal moves from the start
 position). The reference draws them with python-chess, which is not installed here; tests/golden/chess_rules.py is this
 repository's own move generator, pinned by perft and by the reference's encoding known answers.
 

@@ -1,4 +1,4 @@
-"""BASELINE's network configs on the GPU, on seeded random legal positions (tests/golden/positions.npz):
+"""The benchmark's network configs on the GPU, on seeded random legal positions (tests/golden/positions.npz):
 
 - config 3/4, the benchmarked d512 x 28 int8 network exactly as bench.py builds it, against the north star's bars on
   1,024 positions: logits within 2e-2 max-abs, value within 5e-3, the same argmax move on at least 99.9% of the positions
@@ -61,7 +61,7 @@ NOISE = Path(__file__).resolve().parent / "golden" / "network_d512x28_noise.npz"
 
 def check_bars(logits: torch.Tensor, values: torch.Tensor | None, expected_logits: torch.Tensor, expected_values: torch.Tensor, scores=None,
                decidable_gap: float = 0.0, least_raw_agreement: float = 0.999):
-    """The north star's bars (BASELINE.json): logits within 2e-2 max-abs, value within 5e-3, and the same argmax move on at
+    """The north star's bars: logits within 2e-2 max-abs, value within 5e-3, and the same argmax move on at
     least 99.9% of the positions whose argmax is decidable -- the oracle's top two logits further apart than decidable_gap
     -- with least_raw_agreement over all of them."""
     assert (logits - expected_logits).abs().max() < 2e-2
@@ -115,7 +115,7 @@ def test_a_positions_answer_does_not_depend_on_its_batch(benchmarked):
 
 
 def test_config0_the_d256_network_is_the_oracles():
-    """BASELINE config 0's network (d256, 4 blocks: 3 int8 and the fp16 last, 8 heads, SwiGLU 1024) on 64 legal positions."""
+    """Benchmark config 0's network (d256, 4 blocks: 3 int8 and the fp16 last, 8 heads, SwiGLU 1024) on 64 legal positions."""
     model = synthetic_model(CONFIG0, 1)
     state = {name: value.clone() for name, value in model.state_dict().items()}
     weights = nearest_int8_weights(model)

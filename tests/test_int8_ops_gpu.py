@@ -328,7 +328,7 @@ def test_the_split_k_tiles_give_the_whole_k_tiles_bits(device, matmul, out_dtype
 
 
 def config1_case(M: int, K: int, N: int, device):
-    """A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02) (a scale a row), f32 row scales,
+    """benchmark config 1: A int8 uniform in [-127, 127], W int8 rounded from N(0, 0.02) (a scale a row), f32 row scales,
     bias N(0, 0.02), bf16 out."""
     from engine.quantization import nearest
     generator = torch.Generator(device="cpu").manual_seed(M + K + N)
@@ -345,7 +345,7 @@ CONFIG1_SHAPES = [(512, 1536), (512, 512), (512, 2048), (2048, 512)]   # QKV, at
 @pytest.mark.parametrize("K, N", CONFIG1_SHAPES, ids=["qkv", "attention_out", "ffn_up", "ffn_down"])
 @pytest.mark.parametrize("M", [4096, 65536])
 def test_the_config1_gemms_are_the_oracles_in_bf16(device, M, K, N):
-    """The four per-layer shapes of BASELINE config 1 with the bias epilogue and bf16 out, the tile the size picks: every row
+    """The four per-layer shapes of benchmark config 1 with the bias epilogue and bf16 out, the tile the size picks: every row
     against the oracle at M = 4,096; at M = 65,536 the rows of the first, a middle and the last row tile and 256 rows drawn
     across the rest (the oracle's integer product of all 65,536 rows takes minutes)."""
     x, x_scale, weight, weight_scale, bias = config1_case(M, K, N, device)
@@ -452,7 +452,7 @@ def test_template_attention_at_every_value_width_and_token_count(device, heads, 
 
 
 def test_template_attention_at_64_tokens_with_a_bias_per_head(device):
-    """BASELINE config 2's case, per-head bias: templates_count = heads and one-hot coefficients."""
+    """benchmark config 2's case, per-head bias: templates_count = heads and one-hot coefficients."""
     projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps = attention_operands(device, 16, 8, 8, 64, 64, tokens=64)
     c = projected[..., -heads * count:].reshape(16, 64, heads, count)
     c.zero_()
@@ -503,7 +503,7 @@ def bf16_operands(arguments):
 @pytest.mark.parametrize("heads, kv_heads, dq, dv", [(8, 8, 64, 64), (24, 12, 16, 32), (4, 2, 16, 32)])
 @pytest.mark.parametrize("positions, tokens", [(5, 64), (37, 70), (3, 80)])
 def test_bf16_template_attention_is_the_attention_in_fp32(device, heads, kv_heads, dq, dv, positions, tokens):
-    """bf16 rows in and out (BASELINE config 2's types): the fp32 formula of the reference's test on the same bf16 inputs, at
+    """bf16 rows in and out (benchmark config 2's types): the fp32 formula of the reference's test on the same bf16 inputs, at
     config 2's 1e-2 plus the output's own bf16 rounding; the fp16 kernel's answer on them within 1e-2."""
     arguments = bf16_operands(attention_operands(device, positions, heads, kv_heads, dq, dv, seed=positions + tokens, tokens=tokens))
     out = template_attention(*arguments)
@@ -515,7 +515,7 @@ def test_bf16_template_attention_is_the_attention_in_fp32(device, heads, kv_head
 
 
 def test_bf16_template_attention_at_64_tokens_with_a_bias_per_head(device):
-    """BASELINE config 2 in its own types: bf16 Q/K/V and output, a learned 64 x 64 bias per head (one-hot template mix)."""
+    """benchmark config 2 in its own types: bf16 Q/K/V and output, a learned 64 x 64 bias per head (one-hot template mix)."""
     projected, templates, q_gain, k_gain, heads, kv_heads, dq, dv, count, eps = attention_operands(device, 16, 8, 8, 64, 64, tokens=64)
     c = projected[..., -heads * count:].reshape(16, 64, heads, count)
     c.zero_()

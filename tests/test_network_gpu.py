@@ -20,7 +20,7 @@ from model.model import ChessTransformer, expected_score
 pytestmark = pytest.mark.gpu
 
 SMALL = {"d_model": 128, "num_layers": 3, "n_heads": 4, "kv_heads": 2, "qk_ratio": [0.25, 0.5, 0.75], "mlp_hidden": 320, "value_bins": 16}
-# BASELINE's configs 3/4 under the reference's semantics: d512, 28 blocks, 8 heads, SwiGLU 2048
+# the benchmark's configs 3/4 under the reference's semantics: d512, 28 blocks, 8 heads, SwiGLU 2048
 FULL = {"d_model": 512, "num_layers": 28, "n_heads": 8, "mlp_hidden": 2048, "value_bins": 128}
 
 
@@ -104,7 +104,7 @@ def test_the_int8_network_is_the_oracles(device):
 
 
 def test_the_full_size_network_is_the_oracles(device):
-    """BASELINE's d512 x 28 network (27 int8 blocks and the fp16 last) on a few positions."""
+    """The benchmark's d512 x 28 network (27 int8 blocks and the fp16 last) on a few positions."""
     model = make_model(FULL, seed=3)
     compare_with_oracle(model, FULL, random_boards(2, seed=3), device)
 
