@@ -105,11 +105,15 @@ def test_the_benchmarked_network_meets_the_bars_on_1024_positions(benchmarked):
 
 def test_a_positions_answer_does_not_depend_on_its_batch(benchmarked):
     """Batches of 4,096 and 1,024 (the bench's largest and its throughput batch: 286,720 and 71,680 rows, the row kernels'
-    wide launches, the big GEMM tiles) and of 2 (the small tiles), through graphs: a position's answer row is the same
-    bits wherever it sits, the first, a middle and the last row tile of the big batch included."""
+    wide launches, the big GEMM tiles), of 256, 128 and 64 (the split attention slab's smallest launch, the eight-wavefront
+    tiles of down and the fp16 linear, the five-wavefront attention) and of 2 (the small tiles), through graphs: a
+    position's answer row is the same bits wherever it sits, the first, a middle and the last row tile of the big batch
+    included."""
     boards = legal_boards(4096)
     largest = graphed_rows(benchmarked, boards)
     assert torch.equal(graphed_rows(benchmarked, boards[:1024]), largest[:1024])
+    for batch in (256, 128, 64):
+        assert torch.equal(graphed_rows(benchmarked, boards[1024:1024 + batch]), largest[1024:1024 + batch]), batch
     for slots in ([0, 1], [2047, 2048], [4094, 4095], [5, 3000]):
         assert torch.equal(graphed_rows(benchmarked, boards[slots]), largest[slots]), slots
 
