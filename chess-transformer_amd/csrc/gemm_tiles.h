@@ -464,7 +464,7 @@ int launch(const void* x, const void* w, void* out, const Epilogue& e, int M, in
 // The tiles (rows x outputs, wavefronts along M x along N, stages); gated tiles take twice the weight rows.
 // 1: 64 x 64 (2 x 2, 4)    2: 128 x 128 (2 x 2, 4)   3: 128 x 64 (2 x 2, 4)
 // 4: 256 x 128 (4 x 2, 3)  5: 128 x 128 (4 x 2, 2, 128-byte stages)   6: 128 x 128 (4 x 2, 3): eight wavefronts
-// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 256 x 64 (4 x 1, 3)
+// 7: 128 x 128 (2 x 2, 3)  8: 128 x 64 (2 x 2, 3)    9: 128 x 64 (2 x 2, 2)
 // 10: 256 x 64 (4 x 1, 2)  11: 128 x 128 (2 x 2, 2)  12: 128 x 64 (2 x 2, 2) and 13: 128 x 128 (2 x 2, 2) with stages
 // of 128 bytes of K (rows of a multiple of 128 bytes, as tile 5's). 0 picks by the launch's size.
 template <typename In, int NB, typename OutT, bool PACKED, int EPI>
@@ -478,7 +478,7 @@ int by_tile(const void* x, const void* w, void* out, const Epilogue& e, int M, i
         case 6: return launch<In, 128, 128, 4, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 7: return launch<In, 128, 128, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 8: return launch<In, 128, 64, 2, 2, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
-        case 9: return launch<In, 256, 64, 4, 1, NB, 3, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
+        case 9: return launch<In, 128, 64, 2, 2, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 10: return launch<In, 256, 64, 4, 1, NB, 2, OutT, PACKED, EPI>(x, w, out, e, M, N, K, stream);
         case 12: return launch<In, 128, 64, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);
         case 13: return launch<In, 128, 128, 2, 2, NB, 2, OutT, PACKED, EPI, 128>(x, w, out, e, M, N, K, stream);

@@ -26,7 +26,7 @@ INT8_DEPTH = 64
 # The GEMM's tiles by the rows a compute unit's share is (the reference's table format, int8_blocks.py:19-31), timed on an
 # MI355X: 1 is 64 x 64, 2 128 x 128, 3 128 x 64 (rows x outputs, a 4-stage ring), 4 256 x 128, 6 128 x 128 (eight
 # wavefronts, a 3-stage ring), 5 128 x 128 (eight wavefronts, a 2-stage ring of 128-byte stages),
-# 7 128 x 128, 8 128 x 64, 9 256 x 64 (a 3-stage ring), 10 256 x 64, 11 128 x 128 (a 2-stage ring: three workgroups a
+# 7 128 x 128, 8 128 x 64 (a 3-stage ring), 9 128 x 64, 10 256 x 64, 11 128 x 128 (a 2-stage ring: three workgroups a
 # compute unit, which is what the batch-1024 network runs fastest with), 13 128 x 128 (a 2-stage ring of 128-byte stages:
 # down's 2,048-byte rows, read in whole L2 lines), 14 32 x 32 with K split over 4 wavefronts (the reference's small_int8
 # for one or two positions, int8_cuda.py:34-183: in a kernel trace 3.6, 4.3 and 6.2 us where tile 1 takes 4.4, 5.2 and 7.6
@@ -36,9 +36,10 @@ INT8_DEPTH = 64
 # 2.44-2.48 against 2.50-2.53 ms a forward with tile 12, four runs alternated on one box) and up to 48 tile 5 (batch 128:
 # 3.82-3.89 against 3.92-3.97 with tile 11; at batch 256 tile 11 stays ahead in the network). Between 4 and 9 rows a compute unit (batches 15 to 32)
 # projection takes tile 1 and then 8 (batch 16: 0.06 ms a forward faster than tile 11, batch 32: 0.035), and gate_up takes
-# tile 8 up to 18 rows (batch 16 / 32 / 64: 0.05 / 0.03 / 0.045 ms faster than tile 10). Every tile gives the same bits.
+# tile 8, now its 2-stage twin 9, up to 18 rows (batch 16 / 32 / 64: 0.05 / 0.03 / 0.045 ms faster than tile 10; 9 against
+# 8 at batch 64: 2.411-2.432 against 2.420-2.441 ms a forward, six runs alternated on one box). Every tile gives the same bits.
 INT8_TILES = {"gfx950": {"projection": [(0.55, 14), (5, 1), (9, 8), (math.inf, 11)],
-                         "gate_up": [(0.3, 14), (4, 1), (18, 8), (math.inf, 10)],
+                         "gate_up": [(0.3, 14), (4, 1), (18, 9), (math.inf, 10)],
                          "down": [(0.55, 14), (8, 1), (32, 6), (48, 5), (160, 11), (math.inf, 13)]}}
 # the split-K tile's wavefronts: each reads 1, 2 or 4 steps of 128 bytes of K, and the outputs go 8 columns a lane
 SPLIT_WAVES = {14: 4}
