@@ -34,10 +34,10 @@ HBM_PEAK_GBS = 8000.0
 SETTINGS = {"d_model": 512, "num_layers": 28, "n_heads": 8, "kv_heads": 8, "mlp_hidden": 2048, "value_bins": 128, "position_templates": 8}
 TOKENS = 70
 # the GEMM's tiles (rows x outputs, waves, ring stages), as chess_int8_linear numbers them
-GEMM_TILES = {1: "64x64, 4 waves, 4 stages", 2: "128x128, 4 waves, 4 stages", 3: "128x64, 4 waves, 4 stages", 4: "256x128, 4 waves, 3 stages",
-              5: "128x256, 4 waves, 3 stages", 6: "256x64, 4 waves, 4 stages", 7: "128x128, 4 waves, 3 stages", 8: "128x64, 4 waves, 3 stages",
-              9: "256x64, 4 waves, 3 stages", 10: "256x64, 4 waves, 2 stages", 11: "128x128, 4 waves, 2 stages",
-              13: "128x128, 4 waves, 2 stages of 128 bytes", 14: "32x32, K split over 4 waves"}
+GEMM_TILES = {1: "64x64, 4 waves, 4 stages", 2: "128x128, 4 waves, 4 stages", 3: "128x64, 4 waves, 4 stages", 4: "256x128, 8 waves, 3 stages",
+              5: "128x128, 8 waves, 2 stages of 128 bytes", 6: "128x128, 8 waves, 3 stages", 7: "128x128, 4 waves, 3 stages", 8: "128x64, 4 waves, 3 stages",
+              9: "128x64, 4 waves, 2 stages", 10: "256x64, 4 waves, 2 stages", 11: "128x128, 4 waves, 2 stages",
+              12: "128x64, 4 waves, 2 stages of 128 bytes", 13: "128x128, 4 waves, 2 stages of 128 bytes", 14: "32x32, K split over 4 waves"}
 # HBM bytes per launch of the dominant kernel, from rocprofv3 FETCH_SIZE / WRITE_SIZE runs scaled by a plain copy's counters
 TRAFFIC = ROOT / "profiles" / "gate_up_gemm_batch1024_traffic.json"
 COPY_BYTES = 1 << 29
